@@ -1,0 +1,159 @@
+// Page-table metadata kernels and the K/V append scatter.
+//
+//   pkv_get_seq_lens                 <- flashinfer.get_seq_lens              (ecahlang/manager.py:143, 170)
+//   pkv_get_batch_indices_positions  <- flashinfer.get_batch_indices_positions (ecahlang/manager.py:144-146, 171-173)
+//   pkv_append_paged_kv_cache        <- flashinfer.page.append_paged_kv_cache (ecahlang/manager.py:155-165, 175-185, 271-280)
+//
+// The append is pure data movement: every byte of the new K/V rows lands, unchanged, in
+// cache[page][kv][slot][head][:] with page = kv_indices[kv_indptr[b] + pos / page_size] and
+// slot = pos % page_size.  Each lane moves one 16-byte vector (or one element on the
+// misaligned path), K and V rows of every head are handled by one launch, and consecutive
+// lanes cover consecutive bytes of a destination row so both sides coalesce.
+#include "common.h"
+#include "../../include/pagedkv.h"
+
+using namespace pkv;
+
+namespace {
+
+__global__ void seq_lens_kernel(const int32_t* __restrict__ indptr, const int32_t* __restrict__ last,
+                                int32_t batch, int32_t ps, int32_t* __restrict__ out) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  int np = indptr[b + 1] - indptr[b];
+  int full = np - 1 > 0 ? np - 1 : 0;
+  out[b] = full * ps + last[b];
+}
+
+__global__ void batch_positions_kernel(const int32_t* __restrict__ append_indptr,
+                                       const int32_t* __restrict__ seq_lens, int32_t batch,
+                                       int32_t nnz, int32_t* __restrict__ bidx,
+                                       int32_t* __restrict__ pos) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  int b = upper_index(append_indptr, batch, i);
+  int start = append_indptr[b];
+  int len = append_indptr[b + 1] - start;
+  bidx[i] = b;
+  pos[i] = seq_lens[b] - len + (i - start);
+}
+
+// One lane per VEC-byte chunk of a (token, k|v, head) row.  Index order, fastest first:
+// chunk, head, k|v, token -- destination rows of consecutive heads are adjacent in a slot.
+template <int VEC>
+__global__ void append_kernel(const char* __restrict__ k, int64_t k_sn, int64_t k_sh,
+                              const char* __restrict__ v, int64_t v_sn, int64_t v_sh,
+                              const int32_t* __restrict__ bidx, const int32_t* __restrict__ pos,
+                              int32_t nnz, char* __restrict__ k_cache, char* __restrict__ v_cache,
+                              int64_t page_stride, int64_t num_pages,
+                              const int32_t* __restrict__ kv_indices, int64_t num_indices,
+                              const int32_t* __restrict__ kv_indptr, int32_t batch, int32_t hkv,
+                              int32_t row_bytes, int32_t ps, int32_t* __restrict__ err) {
+  using V = typename std::conditional<VEC == 16, uint4,
+            typename std::conditional<VEC == 8, uint2,
+            typename std::conditional<VEC == 4, uint32_t, uint16_t>::type>::type>::type;
+  const int cpr = row_bytes / VEC;
+  const int64_t total = (int64_t)nnz * 2 * hkv * cpr;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    int c = (int)(idx % cpr);
+    int64_t r = idx / cpr;
+    int h = (int)(r % hkv);
+    r /= hkv;
+    int kv = (int)(r & 1);
+    int i = (int)(r >> 1);
+    int b = bidx[i];
+    int p = pos[i];
+    bool ok = b >= 0 && b < batch && p >= 0;
+    int page = -1;
+    if (ok) {
+      int base = kv_indptr[b];
+      int np = kv_indptr[b + 1] - base;
+      int pi = p / ps;
+      ok = pi < np && (int64_t)base + pi < num_indices;
+      if (ok) {
+        page = kv_indices[base + pi];
+        ok = page >= 0 && page < num_pages;
+      }
+    }
+    if (!ok) {  // metadata that points outside the sequence's pages: skip, count it
+      if (c == 0 && err) atomicAdd(err, 1);
+      continue;
+    }
+    int slot = p % ps;
+    const char* src = (kv ? v + i * v_sn + h * v_sh : k + i * k_sn + h * k_sh) + c * VEC;
+    char* dst = (kv ? v_cache : k_cache) + page * page_stride +
+                ((int64_t)slot * hkv + h) * row_bytes + c * VEC;
+    *reinterpret_cast<V*>(dst) = *reinterpret_cast<const V*>(src);
+  }
+}
+
+}  // namespace
+
+extern "C" int pkv_get_seq_lens(const int32_t* kv_indptr, const int32_t* kv_last_page_len,
+                                int32_t batch, int32_t page_size, int32_t* seq_lens,
+                                void* stream) {
+  if (batch < 0 || page_size <= 0) return kBadArg;
+  if (batch == 0) return kOk;
+  int threads = 256, blocks = (batch + threads - 1) / threads;
+  hipLaunchKernelGGL(seq_lens_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream,
+                     kv_indptr, kv_last_page_len, batch, page_size, seq_lens);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_get_batch_indices_positions(const int32_t* append_indptr,
+                                               const int32_t* seq_lens, int32_t batch,
+                                               int32_t nnz, int32_t* batch_indices,
+                                               int32_t* positions, void* stream) {
+  if (batch <= 0 || nnz < 0) return nnz == 0 ? kOk : kBadArg;
+  if (nnz == 0) return kOk;
+  int threads = 256, blocks = (nnz + threads - 1) / threads;
+  hipLaunchKernelGGL(batch_positions_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream,
+                     append_indptr, seq_lens, batch, nnz, batch_indices, positions);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_append_paged_kv_cache(
+    const void* append_key, int64_t k_stride_n, int64_t k_stride_h, const void* append_value,
+    int64_t v_stride_n, int64_t v_stride_h, const int32_t* batch_indices, const int32_t* positions,
+    int32_t nnz, void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
+    const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr, int32_t batch,
+    int32_t num_kv_heads,
+    int32_t head_dim, int32_t page_size, int32_t dtype, int32_t* err_count, void* stream) {
+  int es = dtype == kF32 ? 4 : (dtype == kF16 || dtype == kBF16) ? 2 : 0;
+  if (!es) return kBadDType;
+  if (nnz < 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || batch < 0) return kBadArg;
+  if (nnz == 0) return kOk;
+  // Strides arrive in elements; the kernel works in bytes.
+  int64_t ksn = k_stride_n * es, ksh = k_stride_h * es, vsn = v_stride_n * es, vsh = v_stride_h * es;
+  int64_t pstride = page_stride * es;
+  int row_bytes = head_dim * es;
+  auto aligned = [&](int vec) {
+    uintptr_t m = (uintptr_t)append_key | (uintptr_t)append_value | (uintptr_t)k_cache |
+                  (uintptr_t)v_cache;
+    int64_t s = ksn | ksh | vsn | vsh | pstride | row_bytes;
+    return (m % vec) == 0 && (s % vec) == 0;
+  };
+  int vec = aligned(16) ? 16 : aligned(8) ? 8 : aligned(4) ? 4 : 2;
+  if (vec < es) return kBadAlign;
+  int64_t total = (int64_t)nnz * 2 * num_kv_heads * (row_bytes / vec);
+  int threads = 256;
+  int64_t want = (total + threads - 1) / threads;
+  int blocks = (int)(want < 65536 ? want : 65536);
+  hipStream_t s = (hipStream_t)stream;
+#define PKV_APPEND(VB)                                                                          \
+  hipLaunchKernelGGL(append_kernel<VB>, dim3(blocks), dim3(threads), 0, s,                      \
+                     (const char*)append_key, ksn, ksh, (const char*)append_value, vsn, vsh,    \
+                     batch_indices, positions, nnz, (char*)k_cache, (char*)v_cache, pstride,    \
+                     num_pages, kv_indices, num_indices, kv_indptr, batch, num_kv_heads,        \
+                     row_bytes,                                                                 \
+                     page_size, err_count)
+  switch (vec) {
+    case 16: PKV_APPEND(16); break;
+    case 8: PKV_APPEND(8); break;
+    case 4: PKV_APPEND(4); break;
+    default: PKV_APPEND(2); break;
+  }
+#undef PKV_APPEND
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,141 @@
+"""Seeded synthetic paged-KV workloads: decode and chunked-prefill batches.
+
+Each batch is built the way the serving loop leaves the cache just before the attention
+call: every sequence owns a run of pages taken from a seeded random permutation of the pool,
+the page table follows the FlashInfer convention (last_page_len = (L-1) % page_size + 1), the
+existing context is written into its slots, every other slot of the pool is NaN so a read of
+anything outside the page table shows up in the output, and the new tokens' K/V (plus their
+batch indices and positions) are ready for the append.  Values are generated on the CPU from
+torch.Generator(seed) in fp32 and cast, so a CPU check sees the same bits as the device.
+
+Named shapes (heads q / kv, head_dim, dtype):
+  llama32_1b_fp32   32 / 8 / 64,  float32   (decode, batch 4, context 17, 64, 129, 300)
+  qwen25_3b_fp16    16 / 2 / 128, float16   (decode, batch 64, context U[512, 4096])
+  llama31_8b_bf16   32 / 8 / 128, bfloat16  (decode, batch 128, context log-U[1024, 32768])
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass
+class PagedBatch:
+    hq: int
+    hkv: int
+    d: int
+    ps: int
+    dtype: torch.dtype
+    num_pages: int
+    kv_len: list            # tokens per sequence after the append
+    new_len: list           # appended tokens per sequence (1 for decode, the chunk for prefill)
+    cache: torch.Tensor     # [pages, 2, ps, hkv, d]
+    indptr: torch.Tensor    # int32 [B+1]
+    indices: torch.Tensor   # int32 [sum pages]
+    last: torch.Tensor      # int32 [B]
+    append_indptr: torch.Tensor  # int32 [B+1]
+    batch_indices: torch.Tensor  # int32 [nnz]
+    positions: torch.Tensor      # int32 [nnz]
+    k_new: torch.Tensor     # [nnz, hkv, d]
+    v_new: torch.Tensor     # [nnz, hkv, d]
+    q: torch.Tensor         # [nnz, hq, d] (one row per appended token)
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def batch(self) -> int:
+        return len(self.kv_len)
+
+    def kv_bytes(self) -> int:
+        es = torch.tensor([], dtype=self.dtype).element_size()
+        return sum(self.kv_len) * 2 * self.hkv * self.d * es
+
+    def to(self, device) -> "PagedBatch":
+        kw = {}
+        for name in self.__dataclass_fields__:
+            v = getattr(self, name)
+            kw[name] = v.to(device) if isinstance(v, torch.Tensor) else v
+        return PagedBatch(**kw)
+
+
+def _randn(gen, shape, scale, dtype):
+    return (torch.randn(shape, generator=gen, dtype=torch.float32) * scale).to(dtype)
+
+
+def build_batch(kv_len, new_len, hq, hkv, d, dtype, seed, *, ps=16, scale=1.0,
+                pool_pages=None, pool_factor=1.25, fill_old=True) -> PagedBatch:
+    """CPU-resident batch; call ``.to("cuda")`` for the device copy (bits unchanged)."""
+    gen = torch.Generator().manual_seed(seed)
+    kv_len = [int(x) for x in kv_len]
+    new_len = [int(x) for x in new_len]
+    B = len(kv_len)
+    npages = [(L + ps - 1) // ps for L in kv_len]
+    total_pages = sum(npages)
+    P = pool_pages if pool_pages is not None else max(int(math.ceil(pool_factor * total_pages)), 1)
+    if P < total_pages:
+        raise ValueError("pool smaller than the pages the batch needs")
+    perm = torch.randperm(P, generator=gen).to(torch.int32)
+    indices = perm[:total_pages].clone()
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(npages, dtype=torch.int64), 0).to(torch.int32)
+    last = torch.tensor([((L - 1) % ps) + 1 if L > 0 else 0 for L in kv_len], dtype=torch.int32)
+
+    cache = torch.full((P, 2, ps, hkv, d), float("nan"), dtype=dtype)
+    old_len = [L - n for L, n in zip(kv_len, new_len)]
+    if fill_old and sum(old_len):
+        tok_page, tok_slot = [], []
+        for b in range(B):
+            pos = torch.arange(old_len[b])
+            tok_page.append(indices[indptr[b] + pos // ps].long())
+            tok_slot.append(pos % ps)
+        tp, ts = torch.cat(tok_page), torch.cat(tok_slot)
+        n_old = tp.numel()
+        cache[tp, 0, ts] = _randn(gen, (n_old, hkv, d), scale, dtype)
+        cache[tp, 1, ts] = _randn(gen, (n_old, hkv, d), scale, dtype)
+
+    nnz = sum(new_len)
+    append_indptr = torch.zeros(B + 1, dtype=torch.int32)
+    append_indptr[1:] = torch.cumsum(torch.tensor(new_len, dtype=torch.int64), 0).to(torch.int32)
+    bidx = torch.repeat_interleave(torch.arange(B, dtype=torch.int32),
+                                   torch.tensor(new_len, dtype=torch.int64))
+    pos = torch.cat([torch.arange(o, L, dtype=torch.int32) for o, L in zip(old_len, kv_len)]) \
+        if nnz else torch.zeros(0, dtype=torch.int32)
+    k_new = _randn(gen, (nnz, hkv, d), scale, dtype)
+    v_new = _randn(gen, (nnz, hkv, d), scale, dtype)
+    q = _randn(gen, (nnz, hq, d), scale, dtype)
+    return PagedBatch(hq, hkv, d, ps, dtype, P, kv_len, new_len, cache, indptr, indices, last,
+                      append_indptr, bidx, pos, k_new, v_new, q)
+
+
+def llama32_1b_decode(seed=1001) -> PagedBatch:
+    """32 q / 8 kv heads, head_dim 64, fp32; batch 4 with context 17, 64, 129, 300; pool 256."""
+    ctx = [17, 64, 129, 300]
+    return build_batch([c + 1 for c in ctx], [1] * 4, 32, 8, 64, torch.float32, seed,
+                       pool_pages=256, scale=1.0)
+
+
+def qwen25_3b_decode(seed=1002, batch=64, lo=512, hi=4096) -> PagedBatch:
+    """16 q / 2 kv heads, head_dim 128, fp16; context U[lo, hi]; pool 1.25x the pages used."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    ctx = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
+    return build_batch([c + 1 for c in ctx], [1] * batch, 16, 2, 128, torch.float16, seed,
+                       scale=0.5)
+
+
+def qwen25_3b_prefill(seed=1003, requests=8, chunk=512, max_prefix=8192) -> PagedBatch:
+    """16 q / 2 kv heads, head_dim 128, fp16; each request appends a `chunk`-token chunk onto a
+    paged prefix of U[0, max_prefix] tokens; causal ragged attention over prefix + chunk."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    prefix = torch.randint(0, max_prefix + 1, (requests,), generator=g).tolist()
+    return build_batch([p + chunk for p in prefix], [chunk] * requests, 16, 2, 128,
+                       torch.float16, seed, scale=0.5)
+
+
+def llama31_8b_decode(seed=1004, batch=128, lo=1024, hi=32768, pool_pages=None) -> PagedBatch:
+    """32 q / 8 kv heads, head_dim 128, bf16; context log-uniform in [lo, hi]."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    u = torch.rand(batch, generator=g, dtype=torch.float64)
+    ctx = torch.floor(torch.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))).long().tolist()
+    return build_batch([c + 1 for c in ctx], [1] * batch, 32, 8, 128, torch.bfloat16, seed,
+                       scale=1.0, pool_pages=pool_pages)

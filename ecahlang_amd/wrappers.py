@@ -1,0 +1,233 @@
+"""FlashInfer-shaped batch attention wrappers over the paged cache, backed by libpagedkv.so.
+
+The reference builds one wrapper of each kind on a 128 MiB workspace (ecahlang/main.py:201-204),
+calls ``plan`` once per scheduler step with the step's page table (main.py:341-347, 431-455,
+538-548, 916-922, 963-969) and ``run(q, kv_cache[layer])`` once per layer from the attention
+hook (main.py:68), also inside captured CUDA graphs (main.py:146-148).  The classes below
+keep that call shape:
+
+* ``plan`` reads no device data and launches only one tiny kernel (zeroing the decode
+  workspace counters), so it stays cheap and never synchronises.
+* ``run`` only enqueues kernels on the current stream and is safe to capture in a hipGraph;
+  its geometry (workgroup count, kernel choice) is fixed by ``plan``'s arguments alone.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+
+from ._lib import check, dtype_code, lib, stream_ptr
+from .ops import CacheView, _i32
+
+_STR_DTYPES = {"float16": torch.float16, "half": torch.float16, "bfloat16": torch.bfloat16,
+               "float32": torch.float32, "float": torch.float32}
+
+
+def _as_dtype(d) -> torch.dtype:
+    if isinstance(d, torch.dtype):
+        return d
+    try:
+        return _STR_DTYPES[str(d).replace("torch.", "")]
+    except KeyError:
+        raise ValueError(f"unsupported data type {d!r}") from None
+
+
+def _num_cus(device: torch.device) -> int:
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
+def _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, rope_theta):
+    if str(pos_encoding_mode).upper() != "NONE":
+        raise NotImplementedError("pos_encoding_mode must be 'NONE' (RoPE is applied before the hook)")
+    if window_left is not None and window_left >= 0:
+        raise NotImplementedError("sliding-window attention (window_left >= 0) is not implemented")
+    if logits_soft_cap not in (None, 0, 0.0):
+        raise NotImplementedError("logits_soft_cap is not implemented")
+    if rope_scale is not None or rope_theta is not None:
+        raise NotImplementedError("in-kernel RoPE is not implemented")
+
+
+class BatchDecodeWithPagedKVCacheWrapper:
+    """Paged decode attention: one query token per sequence (FlashInfer contract)."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, use_tensor_cores: bool = False,
+                 paged_kv_indptr_buffer=None, paged_kv_indices_buffer=None,
+                 paged_kv_last_page_len_buffer=None, backend: str = "auto", jit_args=None):
+        if kv_layout.upper() != "NHD":
+            raise NotImplementedError("only the NHD layout is implemented (the reference uses NHD)")
+        if float_workspace_buffer.device.type != "cuda":
+            raise ValueError("workspace must be a CUDA (HIP) tensor")
+        self._workspace = float_workspace_buffer
+        self._kv_layout = "NHD"
+        self._use_cuda_graph = use_cuda_graph
+        self._planned = False
+        self._counters_ready = 0  # batch size whose counters are known to be zero
+
+    @property
+    def is_cuda_graph_enabled(self) -> bool:
+        return self._use_cuda_graph
+
+    def reset_workspace_buffer(self, float_workspace_buffer: torch.Tensor, *_args) -> None:
+        self._workspace = float_workspace_buffer
+        self._counters_ready = 0
+
+    def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+             pos_encoding_mode: str = "NONE", window_left: int = -1, logits_soft_cap=None,
+             q_data_type="float16", kv_data_type=None, data_type=None, sm_scale=None,
+             rope_scale=None, rope_theta=None, non_blocking: bool = True,
+             num_ctas: int | None = None, **_unused) -> None:
+        """``num_ctas`` (an extension) fixes the number of workgroups that share the batch's
+        pages; by default one per compute unit for the matrix-core kernel."""
+        _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, rope_theta)
+        self._indptr = _i32(indptr, "indptr")
+        self._indices = _i32(indices, "indices")
+        self._last = _i32(last_page_len, "last_page_len")
+        self._batch = indptr.numel() - 1
+        if self._last.numel() != self._batch:
+            raise ValueError("last_page_len must have one entry per sequence")
+        if num_qo_heads % num_kv_heads:
+            raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
+        self._hq, self._hkv, self._d, self._ps = int(num_qo_heads), int(num_kv_heads), int(head_dim), int(page_size)
+        if data_type is not None:
+            q_data_type = data_type
+        self._q_dtype = _as_dtype(q_data_type)
+        self._kv_dtype = _as_dtype(kv_data_type) if kv_data_type is not None else self._q_dtype
+        if self._kv_dtype != self._q_dtype:
+            raise NotImplementedError("q and kv must share one dtype")
+        self._sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(self._d)
+        dev = indptr.device
+        self._mfma = bool(lib().pkv_decode_uses_mfma(dtype_code(self._q_dtype), self._d, self._hq,
+                                                     self._hkv)) and self._ps == 16
+        env = os.environ.get("PKV_DECODE_CTAS")
+        if num_ctas is not None:
+            self._ctas = int(num_ctas)
+        elif env:
+            self._ctas = int(env)
+        else:
+            self._ctas = _num_cus(dev) if self._mfma else 2 * _num_cus(dev)
+        if self._ctas <= 0:
+            raise ValueError("num_ctas must be positive")
+        need = lib().pkv_decode_workspace_bytes(self._batch, self._hq, self._d, self._ctas,
+                                                self._indices.numel())
+        if need < 0:
+            check(int(need), "decode plan")
+        if need > self._workspace.numel() * self._workspace.element_size():
+            raise RuntimeError(f"decode workspace too small: need {need} bytes")
+        if self._batch > self._counters_ready:
+            check(lib().pkv_decode_workspace_init(self._workspace.data_ptr(), self._batch,
+                                                  stream_ptr(dev)), "decode plan")
+            self._counters_ready = self._batch
+        self._planned = True
+
+    def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,
+            v_scale=None, out: torch.Tensor | None = None, lse=None, return_lse: bool = False,
+            window_left=None, enable_pdl=None, force_valu: bool = False) -> torch.Tensor:
+        if not self._planned:
+            raise RuntimeError("plan() must be called before run()")
+        if return_lse or lse is not None:
+            raise NotImplementedError("return_lse is not implemented")
+        if q_scale is not None or k_scale is not None or v_scale is not None:
+            raise NotImplementedError("fp8 scales are not implemented")
+        cv = CacheView(paged_kv_cache, self._kv_layout)
+        if q.dim() != 3 or q.shape != (self._batch, self._hq, self._d) or q.stride(2) != 1:
+            raise ValueError(f"q must be [{self._batch}, {self._hq}, {self._d}] with unit inner stride")
+        if q.dtype != self._q_dtype or cv.dtype != self._q_dtype:
+            raise ValueError(f"q / cache dtype must be {self._q_dtype}")
+        if (cv.num_kv_heads, cv.head_dim, cv.page_size) != (self._hkv, self._d, self._ps):
+            raise ValueError("cache geometry differs from plan()")
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+            raise ValueError("out must match q's shape and dtype")
+        check(lib().pkv_batch_decode(
+            q.data_ptr(), q.stride(0), q.stride(1), cv.k_ptr, cv.v_ptr, cv.page_stride, cv.num_pages,
+            self._indptr.data_ptr(), self._indices.data_ptr(), self._indices.numel(),
+            self._last.data_ptr(), self._batch,
+            self._hq, self._hkv, self._d, self._ps, self._sm_scale, self._ctas,
+            self._workspace.data_ptr(), self._workspace.numel() * self._workspace.element_size(),
+            out.data_ptr(), out.stride(0), out.stride(1), dtype_code(q.dtype), int(force_valu),
+            stream_ptr(q.device)), "BatchDecodeWithPagedKVCacheWrapper.run")
+        return out
+
+    forward = run
+
+
+class BatchPrefillWithPagedKVCacheWrapper:
+    """Paged (chunked) prefill attention over ragged query rows (FlashInfer contract)."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, qo_indptr_buf=None, paged_kv_indptr_buf=None,
+                 paged_kv_indices_buf=None, paged_kv_last_page_len_buf=None, custom_mask_buf=None,
+                 mask_indptr_buf=None, backend: str = "auto", jit_args=None):
+        if kv_layout.upper() != "NHD":
+            raise NotImplementedError("only the NHD layout is implemented (the reference uses NHD)")
+        self._workspace = float_workspace_buffer
+        self._kv_layout = "NHD"
+        self._use_cuda_graph = use_cuda_graph
+        self._planned = False
+
+    @property
+    def is_cuda_graph_enabled(self) -> bool:
+        return self._use_cuda_graph
+
+    def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
+             paged_kv_indices: torch.Tensor, paged_kv_last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim_qk: int, page_size: int,
+             head_dim_vo: int | None = None, custom_mask=None, packed_custom_mask=None,
+             causal: bool = False, pos_encoding_mode: str = "NONE",
+             use_fp16_qk_reduction: bool = False, sm_scale=None, window_left: int = -1,
+             logits_soft_cap=None, rope_scale=None, rope_theta=None, q_data_type="float16",
+             kv_data_type=None, non_blocking: bool = True, **_unused) -> None:
+        _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, rope_theta)
+        if custom_mask is not None or packed_custom_mask is not None:
+            raise NotImplementedError("custom masks are not implemented")
+        if head_dim_vo is not None and head_dim_vo != head_dim_qk:
+            raise NotImplementedError("head_dim_vo must equal head_dim_qk")
+        self._qo_indptr = _i32(qo_indptr, "qo_indptr")
+        self._indptr = _i32(paged_kv_indptr, "paged_kv_indptr")
+        self._indices = _i32(paged_kv_indices, "paged_kv_indices")
+        self._last = _i32(paged_kv_last_page_len, "paged_kv_last_page_len")
+        self._batch = paged_kv_indptr.numel() - 1
+        if qo_indptr.numel() != self._batch + 1 or self._last.numel() != self._batch:
+            raise ValueError("qo_indptr / last_page_len disagree with the batch size")
+        if num_qo_heads % num_kv_heads:
+            raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
+        self._hq, self._hkv, self._d, self._ps = int(num_qo_heads), int(num_kv_heads), int(head_dim_qk), int(page_size)
+        self._causal = bool(causal)
+        self._q_dtype = _as_dtype(q_data_type)
+        self._kv_dtype = _as_dtype(kv_data_type) if kv_data_type is not None else self._q_dtype
+        if self._kv_dtype != self._q_dtype:
+            raise NotImplementedError("q and kv must share one dtype")
+        self._sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(self._d)
+        self._planned = True
+
+    def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,
+            v_scale=None, out: torch.Tensor | None = None, lse=None, return_lse: bool = False,
+            enable_pdl=None, window_left=None) -> torch.Tensor:
+        if not self._planned:
+            raise RuntimeError("plan() must be called before run()")
+        if return_lse or lse is not None:
+            raise NotImplementedError("return_lse is not implemented")
+        cv = CacheView(paged_kv_cache, self._kv_layout)
+        if q.dim() != 3 or q.shape[1:] != (self._hq, self._d) or q.stride(2) != 1:
+            raise ValueError(f"q must be [nnz, {self._hq}, {self._d}] with unit inner stride")
+        if q.dtype != self._q_dtype or cv.dtype != self._q_dtype:
+            raise ValueError(f"q / cache dtype must be {self._q_dtype}")
+        if (cv.num_kv_heads, cv.head_dim, cv.page_size) != (self._hkv, self._d, self._ps):
+            raise ValueError("cache geometry differs from plan()")
+        nnz = q.shape[0]
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        check(lib().pkv_batch_prefill_valu(
+            q.data_ptr(), q.stride(0), q.stride(1), self._qo_indptr.data_ptr(), nnz, cv.k_ptr,
+            cv.v_ptr, cv.page_stride, cv.num_pages, self._indptr.data_ptr(),
+            self._indices.data_ptr(), self._indices.numel(), self._last.data_ptr(), self._batch, self._hq, self._hkv, self._d, self._ps,
+            int(self._causal), self._sm_scale, out.data_ptr(), out.stride(0), out.stride(1),
+            dtype_code(q.dtype), stream_ptr(q.device)), "BatchPrefillWithPagedKVCacheWrapper.run")
+        return out
+
+    forward = run

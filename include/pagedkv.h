@@ -1,0 +1,121 @@
+/*
+ * pagedkv.h -- C ABI of libpagedkv.so, the MI355X (gfx950) paged-KV hot path.
+ *
+ * Every pointer is a device pointer owned by the caller (PyTorch tensors' data_ptr()),
+ * every stride is in ELEMENTS, `stream` is a hipStream_t, and no entry point allocates,
+ * frees or synchronises: each call only enqueues kernels on `stream`, so all of them can be
+ * captured into a hipGraph.  Return value: 0 on success, a positive hipError_t from the
+ * launch, or a negative pkv argument code (see PKV_E_* below).
+ *
+ * dtype codes: 0 = float16, 1 = bfloat16, 2 = float32.
+ *
+ * Cache addressing (NHD): element (page, slot, head, dim) of K is
+ *   k_cache[page * page_stride + (slot * num_kv_heads + head) * head_dim + dim]
+ * and likewise for V.  For the reference's single-tensor layer cache
+ * kv_cache[layer] = [pages, 2, page_size, Hkv, D] (ecahlang/manager.py:51-54) pass
+ * k_cache = base, v_cache = base + page_size*Hkv*D, page_stride = 2*page_size*Hkv*D.
+ *
+ * Each entry point replaces one FlashInfer 0.6.5 call made by the reference (FlashInfer is
+ * an external dependency of ecahLang, pinned at uv.lock:324-325; the call sites cited are
+ * the reference's).
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_E_DTYPE (-1)
+#define PKV_E_HEAD_DIM (-2)
+#define PKV_E_GROUP (-3)
+#define PKV_E_ALIGN (-4)
+#define PKV_E_ARG (-5)
+#define PKV_E_WORKSPACE (-6)
+#define PKV_E_PAGE_SIZE (-7)
+
+/* flashinfer.get_seq_lens(kv_indptr, kv_last_page_len, page_size)
+ * (ecahlang/manager.py:143, :170):
+ * seq_lens[b] = max(kv_indptr[b+1] - kv_indptr[b] - 1, 0) * page_size + kv_last_page_len[b]. */
+int pkv_get_seq_lens(const int32_t* kv_indptr, const int32_t* kv_last_page_len, int32_t batch,
+                     int32_t page_size, int32_t* seq_lens, void* stream);
+
+/* flashinfer.get_batch_indices_positions(append_indptr, seq_lens, nnz)
+ * (ecahlang/manager.py:144-146, :171-173): for appended token i of request b,
+ * batch_indices[i] = b and
+ * positions[i] = seq_lens[b] - (append_indptr[b+1] - append_indptr[b]) + (i - append_indptr[b]). */
+int pkv_get_batch_indices_positions(const int32_t* append_indptr, const int32_t* seq_lens,
+                                    int32_t batch, int32_t nnz, int32_t* batch_indices,
+                                    int32_t* positions, void* stream);
+
+/* flashinfer.page.append_paged_kv_cache(append_key, append_value, batch_indices, positions,
+ * paged_kv_cache, kv_indices, kv_indptr, kv_last_page_len, kv_layout="NHD")
+ * (ecahlang/manager.py:155-165, :175-185, :271-280).  append_key/value are [nnz, Hkv, D]
+ * with strides (stride_n, stride_h) and a unit inner stride.  Token i goes to page
+ * kv_indices[kv_indptr[b] + positions[i] / page_size], slot positions[i] % page_size, where
+ * b = batch_indices[i].  A token whose metadata points outside its sequence's pages, past
+ * num_indices entries of kv_indices, or outside the num_pages-page pool is skipped and
+ * counted in *err_count (may be NULL) instead of written. */
+int pkv_append_paged_kv_cache(const void* append_key, int64_t k_stride_n, int64_t k_stride_h,
+                              const void* append_value, int64_t v_stride_n, int64_t v_stride_h,
+                              const int32_t* batch_indices, const int32_t* positions, int32_t nnz,
+                              void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
+                              const int32_t* kv_indices, int64_t num_indices,
+                              const int32_t* kv_indptr, int32_t batch,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                              int32_t dtype, int32_t* err_count, void* stream);
+
+/* Workspace bytes pkv_batch_decode needs for this geometry (num_indices = length of the
+ * kv_indices buffer): the host half of BatchDecodeWithPagedKVCacheWrapper.plan
+ * (ecahlang/main.py:341-347, :444-455).  The reference hands the wrapper a 128 MiB buffer
+ * (ecahlang/main.py:203). */
+int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
+                                   int32_t num_ctas, int64_t num_indices);
+
+/* Zeroes the split-merge counters at the head of the workspace (the device half of plan).
+ * pkv_batch_decode leaves them zero again when it finishes, so this is needed only when the
+ * buffer is fresh or the batch grows. */
+int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream);
+
+/* 1 when pkv_batch_decode runs the matrix-core kernel for this shape (fp16/bf16, head_dim 64
+ * or 128, page_size 16, group <= 16, num_kv_heads <= 8), 0 when it runs the vector-ALU kernel. */
+int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
+                         int32_t num_kv_heads);
+
+/* BatchDecodeWithPagedKVCacheWrapper.run(q, paged_kv_cache) (ecahlang/main.py:68, captured
+ * at :162-171): out[b, h, :] = softmax(q[b,h] . K_b^T * sm_scale) V_b over the
+ * seq_len_b = (npages_b - 1) * page_size + kv_last_page_len[b] tokens of sequence b, with
+ * KV head h / (num_qo_heads / num_kv_heads); fp32 accumulation, output in `dtype`.  A
+ * sequence with no tokens yields zeros.  num_ctas workgroups each stream an equal share of
+ * the batch's pages; force_valu = 1 selects the vector-ALU kernel for cross-checks.  Page
+ * ids outside [0, num_pages) and page-list entries past num_indices are never read (their
+ * tokens are treated as absent). */
+int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k_cache,
+                     const void* v_cache, int64_t page_stride, int64_t num_pages,
+                     const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
+                     const int32_t* kv_last_page_len, int32_t batch,
+                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t page_size, float sm_scale, int32_t num_ctas, void* workspace,
+                     int64_t workspace_bytes, void* out, int64_t o_stride_n, int64_t o_stride_h,
+                     int32_t dtype, int32_t force_valu, void* stream);
+
+/* BatchPrefillWithPagedKVCacheWrapper.run(q, paged_kv_cache) after
+ * plan(qo_indptr, kv_indptr, kv_indices, kv_last_page_len, ..., causal=...)
+ * (ecahlang/main.py:432-443, :68), vector-ALU kernel: query row i of request b
+ * (qo_len_b = qo_indptr[b+1] - qo_indptr[b]) attends keys j <= i + kv_len_b - qo_len_b when
+ * causal != 0 (bottom-right aligned), else all kv_len_b keys. */
+int pkv_batch_prefill_valu(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                           const int32_t* qo_indptr, int32_t nnz_q, const void* k_cache,
+                           const void* v_cache, int64_t page_stride, int64_t num_pages,
+                           const int32_t* kv_indptr, const int32_t* kv_indices,
+                           int64_t num_indices, const int32_t* kv_last_page_len,
+                           int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t page_size, int32_t causal, float sm_scale,
+                           void* out, int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PAGEDKV_H */

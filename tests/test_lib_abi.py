@@ -1,0 +1,53 @@
+"""The C-ABI library loads and exports exactly what include/pagedkv.h declares (CPU only:
+loading the library and resolving symbols makes no GPU call)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "pagedkv.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "pkv_batch_decode" in names and "pkv_append_paged_kv_cache" in names
+    assert len(names) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    from ecahlang_amd import _lib
+
+    h = _lib.lib()
+    missing = [n for n in _declared() if not hasattr(h, n)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    from ecahlang_amd import _lib
+
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_loader_refuses_missing_library(monkeypatch, tmp_path):
+    from ecahlang_amd import _lib
+
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    with pytest.raises(RuntimeError, match="no CPU or PyTorch fallback"):
+        _lib.lib()
+
+
+def test_workspace_sizing_is_host_only():
+    from ecahlang_amd import _lib
+
+    n = _lib.lib().pkv_decode_workspace_bytes(64, 16, 128, 256, 12000)
+    assert n >= (256 + 64) * 16 * 128 * 4
+    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2) == 1
+    assert _lib.lib().pkv_decode_uses_mfma(2, 64, 32, 8) == 0
