@@ -64,37 +64,103 @@ __device__ __forceinline__ int seq_len_of(const DecodeParams& P, int b) {
   return np > 0 ? (np - 1) * P.ps + P.last[b] : 0;
 }
 
-// Cross-workgroup data (split partials, arrival counters) moves only through device-scope
-// atomic loads and stores.  Those are coherent across the XCDs' separate L2 caches by
-// themselves, so the hand-off needs no L2 write-back / invalidate (which a device-scope
-// fence would issue, once per segment per workgroup): a writer waits for its stores to
-// complete before bumping the counter, and the last arriver reads with device-scope loads.
+// Cross-workgroup hand-off of split partials without device-scope fences (each of which
+// writes back and invalidates a whole L2, once per segment per workgroup):
+//  * writers store partials with device-scope atomic stores, which write through the
+//    XCD's L2, and wait for them to complete before bumping the sequence's counter;
+//  * the last arriver then reads them with plain loads: no L2 on its XCD has held those
+//    lines since the kernel began (each partial slot is read once, by that merger only,
+//    and caches start the kernel invalidated), so the loads fetch the written values, and
+//    being plain they can all be in flight at once.
 __device__ __forceinline__ void st_dev(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_dev(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// 16-byte device-scope (write-through, sc1) vector store: the same effect as four st_dev,
+// issued as a buffer store with the sc1 cache policy so the compiler still tracks its
+// register hazards (a hand-written store can have its data registers reused before the
+// hardware has read them).  `base` is the start of the partial area, `off` a byte offset.
+typedef float fvec4 __attribute__((ext_vector_type(4)));
+constexpr int kCpolSc1 = 16;  // device scope: write through this XCD's L2
+__device__ __forceinline__ void st_dev4(float* base, uint32_t off, fvec4 v) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCpolSc1);
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Merge the partial states of sequence b (workgroups w_lo..w_hi) into the output row.
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() also carries a release fence,
+// which on this target waits for every outstanding global load (vmcnt(0)) and so would
+// drain each wave's K/V prefetch at every barrier; here only LDS traffic is settled.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Merge of sequence b's partials in one round of loads: every thread owns 4 consecutive
+// output dims of one head and issues the loads of all segments' (max, sum) and partial
+// rows up front (nseg <= kMergeRegs), then folds them in registers.
+constexpr int kMergeRegs = 8;
+template <typename T, int D>
+__device__ void merge_partials_regs(const DecodeParams& P, int b, int w_lo, int w_hi) {
+  T* out = reinterpret_cast<T*>(P.out);
+  const int nseg = w_hi - w_lo + 1;
+  const int64_t s0 = (int64_t)(w_lo + b) * P.hq;
+  for (int idx = threadIdx.x; idx < P.hq * (D / 4); idx += blockDim.x) {
+    const int h = idx / (D / 4), d = (idx - h * (D / 4)) * 4;
+    float2 ml[kMergeRegs];
+    float4 po[kMergeRegs];
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s < nseg) {
+        ml[s] = P.part_ml[s0 + (int64_t)s * P.hq + h];
+        po[s] = *reinterpret_cast<const float4*>(P.part_o + (s0 + (int64_t)s * P.hq + h) * D + d);
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s)
+      if (s < nseg) M = fmaxf(M, ml[s].x);
+    float den = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s < nseg) {
+        const float c = ml[s].y > 0.f ? exp2f(ml[s].x - M) * ml[s].y : 0.f;
+        den += c;
+        acc.x += c * po[s].x;
+        acc.y += c * po[s].y;
+        acc.z += c * po[s].z;
+        acc.w += c * po[s].w;
+      }
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    T* orow = out + b * P.o_sn + h * P.o_sh + d;
+    orow[0] = from_f32<T>(acc.x * inv);
+    orow[1] = from_f32<T>(acc.y * inv);
+    orow[2] = from_f32<T>(acc.z * inv);
+    orow[3] = from_f32<T>(acc.w * inv);
+  }
+}
+
+// Merge of sequence b's partials straight from global memory (any segment count).
 template <typename T, int D>
 __device__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi) {
   T* out = reinterpret_cast<T*>(P.out);
-  const float* ml = reinterpret_cast<const float*>(P.part_ml);
+  const int nseg = w_hi - w_lo + 1;
+  const int64_t s0 = (int64_t)(w_lo + b) * P.hq;
   for (int idx = threadIdx.x; idx < P.hq * D; idx += blockDim.x) {
-    int h = idx / D, d = idx - h * D;
+    const int h = idx / D, d = idx - h * D;
+    const float2* ml = P.part_ml + s0 + h;
+    const float* po = P.part_o + (s0 + h) * D + d;
     float M = -INFINITY;
-    for (int w = w_lo; w <= w_hi; ++w) M = fmaxf(M, ld_dev(ml + 2 * ((int64_t)(w + b) * P.hq + h)));
+#pragma unroll 4
+    for (int s = 0; s < nseg; ++s) M = fmaxf(M, ml[(int64_t)s * P.hq].x);
     float num = 0.f, den = 0.f;
-    for (int w = w_lo; w <= w_hi; ++w) {
-      int64_t s = (int64_t)(w + b) * P.hq + h;
-      float mx = ld_dev(ml + 2 * s), l = ld_dev(ml + 2 * s + 1);
-      if (l > 0.f) {
-        float c = exp2f(mx - M) * l;
-        num += c * ld_dev(P.part_o + s * D + d);
-        den += c;
-      }
+#pragma unroll 4
+    for (int s = 0; s < nseg; ++s) {
+      const float2 v = ml[(int64_t)s * P.hq];
+      const float o = po[(int64_t)s * P.hq * D];
+      const float c = v.y > 0.f ? exp2f(v.x - M) * v.y : 0.f;
+      num += c * o;
+      den += c;
     }
     out[b * P.o_sn + h * P.o_sh + d] = from_f32<T>(den > 0.f ? num / den : 0.f);
   }
@@ -156,6 +222,17 @@ __device__ __forceinline__ int decode_ranges(int num_ctas, int64_t total) {
   return (int)(n > need ? n : need);
 }
 
+// Largest b in [0, n) with a[b] <= x over an LDS copy of indptr (a[0] <= x assumed);
+// the result is wave-uniform.
+__device__ __forceinline__ int lds_upper_index(const int* a, int n, int64_t x) {
+  int lo = 0, hi = n;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if ((int64_t)a[mid] <= x) lo = mid; else hi = mid;
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
 // Largest b in [0, B) with indptr[b] <= p, found by the whole wave: each lane loads one
 // entry and a ballot counts the prefix (indptr is non-decreasing), so B <= 64 costs one
 // round of loads and B <= 4096 two.
@@ -176,6 +253,6 @@ __device__ __forceinline__ int find_seq_wave(const int32_t* indptr, int B, int64
 
 int decode_valu_dispatch(const DecodeParams& P, int dtype, int d, hipStream_t s);
 int decode_mfma_dispatch(const DecodeParams& P, int dtype, int d, hipStream_t s);
-bool decode_mfma_supported(int dtype, int d, int g, int hkv);
+bool decode_mfma_supported(int dtype, int d, int g, int hkv, int batch);
 
 }  // namespace pkv

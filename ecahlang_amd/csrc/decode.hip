@@ -52,9 +52,10 @@ extern "C" int pkv_decode_workspace_init(void* workspace, int32_t batch, void* s
 }
 
 extern "C" int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
-                                    int32_t num_kv_heads) {
+                                    int32_t num_kv_heads, int32_t batch) {
   if (num_kv_heads <= 0 || num_qo_heads % num_kv_heads) return 0;
-  return decode_mfma_supported(dtype, head_dim, num_qo_heads / num_kv_heads, num_kv_heads) ? 1 : 0;
+  return decode_mfma_supported(dtype, head_dim, num_qo_heads / num_kv_heads, num_kv_heads, batch)
+             ? 1 : 0;
 }
 
 extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h,
@@ -93,7 +94,7 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   P.o_vec = ((uintptr_t)out % 8 == 0) && ((o_stride_n * es) % 8 == 0) && ((o_stride_h * es) % 8 == 0);
   hipStream_t s = (hipStream_t)stream;
   int g = num_qo_heads / num_kv_heads;
-  if (!force_valu && decode_mfma_supported(dtype, head_dim, g, num_kv_heads))
+  if (!force_valu && decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
     return decode_mfma_dispatch(P, dtype, head_dim, s);
   return decode_valu_dispatch(P, dtype, head_dim, s);
 }

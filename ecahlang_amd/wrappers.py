@@ -101,7 +101,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(self._d)
         dev = indptr.device
         self._mfma = bool(lib().pkv_decode_uses_mfma(dtype_code(self._q_dtype), self._d, self._hq,
-                                                     self._hkv)) and self._ps == 16
+                                                     self._hkv, self._batch)) and self._ps == 16
         env = os.environ.get("PKV_DECODE_CTAS")
         if num_ctas is not None:
             self._ctas = int(num_ctas)

@@ -79,9 +79,10 @@ int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t 
 int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream);
 
 /* 1 when pkv_batch_decode runs the matrix-core kernel for this shape (fp16/bf16, head_dim 64
- * or 128, page_size 16, group <= 16, num_kv_heads <= 8), 0 when it runs the vector-ALU kernel. */
+ * or 128, page_size 16, group <= 16, num_kv_heads <= 8, batch <= 2048), 0 when it runs the
+ * vector-ALU kernel. */
 int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
-                         int32_t num_kv_heads);
+                         int32_t num_kv_heads, int32_t batch);
 
 /* BatchDecodeWithPagedKVCacheWrapper.run(q, paged_kv_cache) (ecahlang/main.py:68, captured
  * at :162-171): out[b, h, :] = softmax(q[b,h] . K_b^T * sm_scale) V_b over the

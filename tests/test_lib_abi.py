@@ -49,5 +49,6 @@ def test_workspace_sizing_is_host_only():
 
     n = _lib.lib().pkv_decode_workspace_bytes(64, 16, 128, 256, 12000)
     assert n >= (256 + 64) * 16 * 128 * 4
-    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2) == 1
-    assert _lib.lib().pkv_decode_uses_mfma(2, 64, 32, 8) == 0
+    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 64) == 1
+    assert _lib.lib().pkv_decode_uses_mfma(2, 64, 32, 8, 4) == 0
+    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 4096) == 0
