@@ -290,12 +290,6 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
 #pragma unroll
     for (int r = 0; r < VCH; ++r) vr[r] = *reinterpret_cast<const uint4*>(vb + voff[r]);
   };
-  // Ping-pong buffers: page k lives in A when k is even, B when odd; two pages in flight.
-  uint4 kA[KSTEPS], vA[VCH], kB[KSTEPS], vB[VCH];
-  if (nk > 0) {
-    load_page(pid_of(0), kA, vA);
-    load_page(pid_of(1), kB, vB);  // nk == 1 reloads page 0: harmless, keeps the pipeline uniform
-  }
 
   // ---- the range's pages, one loop per wave; sequence (segment) boundaries are crossed
   // inside it.  Every wave ends each segment of the range once and in order, so the
@@ -496,6 +490,14 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
     __builtin_amdgcn_sched_barrier(0);
   };
   start_segment();
+  // Ping-pong buffers: page k lives in A when k is even, B when odd; two pages in flight.
+  // Issued only now, after the scalar set-up: work between these loads and their first use
+  // risks a wait that drains them.
+  uint4 kA[KSTEPS], vA[VCH], kB[KSTEPS], vB[VCH];
+  if (nk > 0) {
+    load_page(pid_of(0), kA, vA);
+    load_page(pid_of(1), kB, vB);  // nk == 1 reloads page 0: harmless, keeps the pipeline uniform
+  }
   for (int k = 0; k < nk; k += 2) {
     step(kA, vA, k);
     if (k + 1 < nk) step(kB, vB, k + 1);
