@@ -35,22 +35,30 @@ struct DecodeParams {
   int32_t num_ctas;
   int32_t q_vec;               // q rows / strides allow 16-byte loads
   int32_t o_vec;               // out rows / strides allow 8-byte stores
+  int32_t dynamic;             // matrix-core kernel: waves take pages on demand
 };
 
-__device__ __forceinline__ int64_t range_start(int w, int n, int64_t total) {
-  return (int64_t)w * total / n;
-}
-// Workgroup whose range holds page p (largest w with range_start(w) <= p).
-__device__ __forceinline__ int range_owner(int64_t p, int n, int64_t total) {
-  int64_t w = ((p + 1) * n + total - 1) / total - 1;
-  return (int)(w < n - 1 ? w : n - 1);
-}
+// Partition of the batch's `total` pages into n contiguous ranges (1 <= n <= total): the
+// first r = total % n ranges hold q + 1 pages, the others q = total / n.  32-bit arithmetic
+// only (total < 2^31 as page-list offsets are int32): a 64-bit division is a long software
+// sequence on this target.
+struct Ranges {
+  int n, q, r, big;  // big = r * (q + 1): first page of the q-page ranges
+  __device__ __forceinline__ Ranges(int n_, int total)
+      : n(n_), q(total / n_), r(total % n_), big((total % n_) * (total / n_ + 1)) {}
+  __device__ __forceinline__ int start(int w) const { return w * q + (w < r ? w : r); }
+  // Range holding page p (clamped to the last range for p >= total).
+  __device__ __forceinline__ int owner(int p) const {
+    const int w = p < big ? p / (q + 1) : r + (p - big) / q;
+    return w < n - 1 ? w : n - 1;
+  }
+};
 
 // Total pages of the batch, cut to the length of the indices array.
-__device__ __forceinline__ int64_t total_pages(const DecodeParams& P) {
+__device__ __forceinline__ int total_pages(const DecodeParams& P) {
   int64_t t = P.indptr[P.batch];
   t = t < P.num_indices ? t : P.num_indices;
-  return t > 0 ? t : 0;
+  return t > 0 ? (int)t : 0;
 }
 
 // Page id at position i of the concatenated page list, or -1 when it is outside the pool.
@@ -94,37 +102,52 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Merge of sequence b's partials in one round of loads: every thread owns 4 consecutive
-// output dims of one head and issues the loads of all segments' (max, sum) and partial
-// rows up front (nseg <= kMergeRegs), then folds them in registers.
-constexpr int kMergeRegs = 8;
+constexpr int kMergeRegs = 8;  // segments a merge folds from registers
+
+// Merges of the sequences queued in `list` (rows of sequence, w_lo, w_hi), all at once.
+// An item is 4 consecutive output dims of one head of one queued sequence; each thread
+// takes two items per round and issues both items' loads before folding either, so the
+// whole queue costs about one memory latency per 2 * blockDim.x items.  Sequences with
+// more than kMergeRegs segments are merged afterwards from global memory.
 template <typename T, int D>
-__device__ void merge_partials_regs(const DecodeParams& P, int b, int w_lo, int w_hi) {
-  T* out = reinterpret_cast<T*>(P.out);
-  const int nseg = w_hi - w_lo + 1;
-  const int64_t s0 = (int64_t)(w_lo + b) * P.hq;
-  for (int idx = threadIdx.x; idx < P.hq * (D / 4); idx += blockDim.x) {
-    const int h = idx / (D / 4), d = (idx - h * (D / 4)) * 4;
-    float2 ml[kMergeRegs];
-    float4 po[kMergeRegs];
+struct MergeItem {
+  float2 ml[kMergeRegs];
+  float4 po[kMergeRegs];
+  int b = -1, h = 0, d = 0, nseg = 0;
+  // Item `item` of `nitems` (>= 1).  Every load is issued, from clamped indices, whether or
+  // not the item is real (item >= nitems) or short of kMergeRegs segments: a load under a
+  // branch gets a wait for its result at the branch's end, which would serialise them.
+  __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int per, int item,
+                                       int nitems) {
+    const bool real = item < nitems;
+    const int it = real ? item : nitems - 1;
+    const int i = it / per, r = it - i * per;
+    const int bb = list[i][0], lo = list[i][1];
+    nseg = list[i][2] - lo + 1;
+    b = (real && nseg <= kMergeRegs) ? bb : -1;  // longer ones are merged from global memory
+    const int ns = nseg < kMergeRegs ? nseg : kMergeRegs;
+    h = r / (D / 4);
+    d = (r - h * (D / 4)) * 4;
+    const int64_t s0 = (int64_t)(lo + bb) * P.hq + h;
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
-      if (s < nseg) {
-        ml[s] = P.part_ml[s0 + (int64_t)s * P.hq + h];
-        po[s] = *reinterpret_cast<const float4*>(P.part_o + (s0 + (int64_t)s * P.hq + h) * D + d);
-      }
+      const int64_t e = s0 + (int64_t)(s < ns ? s : ns - 1) * P.hq;
+      ml[s] = P.part_ml[e];
+      po[s] = *reinterpret_cast<const float4*>(P.part_o + e * D + d);
     }
+  }
+  __device__ __forceinline__ void finish(const DecodeParams& P) const {
+    if (b < 0) return;
     float M = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < kMergeRegs; ++s)
-      if (s < nseg) M = fmaxf(M, ml[s].x);
+    for (int s = 0; s < kMergeRegs; ++s) M = s < nseg ? fmaxf(M, ml[s].x) : M;
     float den = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
-      if (s < nseg) {
-        const float c = ml[s].y > 0.f ? exp2f(ml[s].x - M) * ml[s].y : 0.f;
-        den += c;
+      const float c = (s < nseg && ml[s].y > 0.f) ? exp2f(ml[s].x - M) * ml[s].y : 0.f;
+      den += c;
+      if (c != 0.f) {  // (a dropped segment's row may hold anything)
         acc.x += c * po[s].x;
         acc.y += c * po[s].y;
         acc.z += c * po[s].z;
@@ -132,17 +155,43 @@ __device__ void merge_partials_regs(const DecodeParams& P, int b, int w_lo, int 
       }
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    T* orow = out + b * P.o_sn + h * P.o_sh + d;
-    orow[0] = from_f32<T>(acc.x * inv);
-    orow[1] = from_f32<T>(acc.y * inv);
-    orow[2] = from_f32<T>(acc.z * inv);
-    orow[3] = from_f32<T>(acc.w * inv);
+    T* orow = reinterpret_cast<T*>(P.out) + b * P.o_sn + h * P.o_sh + d;
+    if (sizeof(T) == 2 && P.o_vec) {
+      T v[4] = {from_f32<T>(acc.x * inv), from_f32<T>(acc.y * inv), from_f32<T>(acc.z * inv),
+                from_f32<T>(acc.w * inv)};
+      *reinterpret_cast<uint2*>(orow) = *reinterpret_cast<const uint2*>(v);
+    } else {
+      orow[0] = from_f32<T>(acc.x * inv);
+      orow[1] = from_f32<T>(acc.y * inv);
+      orow[2] = from_f32<T>(acc.z * inv);
+      orow[3] = from_f32<T>(acc.w * inv);
+    }
   }
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi);
+
+template <typename T, int D>
+__device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*list)[3], int nm) {
+  const int per = P.hq * (D / 4);
+  const int nitems = nm * per;
+  const int nt = blockDim.x;
+  for (int base = 0; base < nitems; base += 2 * nt) {
+    const int i0 = base + threadIdx.x, i1 = i0 + nt;
+    MergeItem<T, D> a, c;
+    a.load(P, list, per, i0, nitems);
+    c.load(P, list, per, i1, nitems);
+    a.finish(P);
+    c.finish(P);
+  }
+  for (int i = 0; i < nm; ++i)
+    if (list[i][2] - list[i][1] + 1 > kMergeRegs) merge_partials<T, D>(P, list[i][0], list[i][1], list[i][2]);
 }
 
 // Merge of sequence b's partials straight from global memory (any segment count).
 template <typename T, int D>
-__device__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi) {
+__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi) {
   T* out = reinterpret_cast<T*>(P.out);
   const int nseg = w_hi - w_lo + 1;
   const int64_t s0 = (int64_t)(w_lo + b) * P.hq;
@@ -194,7 +243,7 @@ __device__ __forceinline__ bool arrive_last(const DecodeParams& P, int b, int ns
 // Zero the output rows of sequences that own no pages (no workgroup range touches them).
 // One thread per sequence, so the check costs one round of loads, not one per sequence.
 template <typename T, int D>
-__device__ void zero_empty_sequences(const DecodeParams& P) {
+__device__ __forceinline__ void zero_empty_sequences(const DecodeParams& P) {
   T* out = reinterpret_cast<T*>(P.out);
   for (int b = threadIdx.x; b < P.batch; b += blockDim.x) {
     if (P.indptr[b + 1] > P.indptr[b]) continue;
@@ -204,9 +253,9 @@ __device__ void zero_empty_sequences(const DecodeParams& P) {
 }
 
 // Number of page ranges actually used: never more ranges than pages, so no range is empty
-// and the workgroups touching a sequence are exactly range_owner(first)..range_owner(last).
-__device__ __forceinline__ int effective_ranges(int num_ctas, int64_t total) {
-  return (int)(num_ctas < total ? num_ctas : total);
+// and the workgroups touching a sequence are exactly Ranges::owner(first)..owner(last).
+__device__ __forceinline__ int effective_ranges(int num_ctas, int total) {
+  return num_ctas < total ? num_ctas : total;
 }
 
 // The matrix-core kernel also caps a range at kPidCap pages (its page ids are staged in
@@ -216,10 +265,10 @@ __host__ __device__ __forceinline__ int64_t decode_ranges_max(int num_ctas, int6
   int64_t need = (total + kPidCap - 1) / kPidCap;
   return need > num_ctas ? need : num_ctas;
 }
-__device__ __forceinline__ int decode_ranges(int num_ctas, int64_t total) {
-  int64_t n = total < num_ctas ? total : num_ctas;
-  int64_t need = (total + kPidCap - 1) / kPidCap;
-  return (int)(n > need ? n : need);
+__device__ __forceinline__ int decode_ranges(int num_ctas, int total) {
+  const int n = total < num_ctas ? total : num_ctas;
+  const int need = (int)(((unsigned)total + kPidCap - 1) / kPidCap);
+  return n > need ? n : need;
 }
 
 // Largest b in [0, n) with a[b] <= x over an LDS copy of indptr (a[0] <= x assumed);

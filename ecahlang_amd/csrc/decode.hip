@@ -67,7 +67,7 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
                                 int32_t page_size, float sm_scale, int32_t num_ctas,
                                 void* workspace, int64_t workspace_bytes, void* out,
                                 int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
-                                int32_t force_valu, void* stream) {
+                                int32_t flags, void* stream) {
   if (batch <= 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_ctas <= 0) return kBadArg;
   if (num_qo_heads % num_kv_heads) return kBadGroup;
   if (page_size <= 0) return kBadPageSize;
@@ -89,12 +89,13 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   P.part_ml = (float2*)(ws + L.ml);
   P.part_o = (float*)(ws + L.o);
   P.num_ctas = num_ctas;
+  P.dynamic = (flags & PKV_DECODE_DYNAMIC) != 0;
   const int es = dtype == kF32 ? 4 : 2;
   P.q_vec = ((uintptr_t)q % 16 == 0) && ((q_stride_n * es) % 16 == 0) && ((q_stride_h * es) % 16 == 0);
   P.o_vec = ((uintptr_t)out % 8 == 0) && ((o_stride_n * es) % 8 == 0) && ((o_stride_h * es) % 8 == 0);
   hipStream_t s = (hipStream_t)stream;
   int g = num_qo_heads / num_kv_heads;
-  if (!force_valu && decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
+  if (!(flags & PKV_DECODE_VALU) && decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
     return decode_mfma_dispatch(P, dtype, head_dim, s);
   return decode_valu_dispatch(P, dtype, head_dim, s);
 }

@@ -19,8 +19,9 @@
 //                                       copy of the page (coalesced 16-byte HBM loads)
 // The reduction index of both products only has to agree between the two operands, so the
 // dim order inside K and Q operands is chosen to make each K load 64 contiguous bytes.
-// Waves of one workgroup split the pages of each segment; their states meet in LDS by a
-// pairwise tree, and the last wave writes the output (or the partial for a split sequence).
+// Waves of one workgroup split the pages of each segment; their states meet in LDS at the
+// segment's end, where every wave folds the copies of the output tiles it owns and writes
+// them (as output rows, or as the partial of a sequence split across workgroups).
 #include "attn_common.h"
 #include "../../include/pagedkv.h"
 
@@ -93,9 +94,10 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
 }
 
 // Dynamic LDS of the kernel, in bytes (host and device compute the same layout):
-//   tiles  one V page per wave, XOR-swizzled                       W * 16 * D * 2
-//   slots  online-softmax state of every wave that is not its
-//          head's leader (j > 0), parked for the leader's combine  (W - W/J) * XCH * 256
+//   tiles  one V page per wave, XOR-swizzled                        W * 16 * D * 2
+//   slots  softmax states met at a segment end: (max, sum) of every
+//          wave, and each output tile of a head from the J - 1 waves
+//          that do not own it                                        W * 512 + hkv * (J - 1) * MT * 1024
 //   meta   indptr[0..B] and last_page_len[0..B) (B <= kMetaCap)
 //   q      query rows of the range's first qseg sequences, plus one slot filled on demand
 //          for a range with more segments
@@ -106,16 +108,17 @@ constexpr int kQSegMax = 4;
 __host__ __device__ constexpr int align_up(int x, int a) { return (x + a - 1) / a * a; }
 
 struct MfmaLds {
-  int tiles, slots, meta, q, total;
+  int tiles, slots, copies, meta, q, total;
 };
 template <int D, int W>
 __host__ __device__ inline MfmaLds mfma_lds(int hkv, int hq, int qseg) {
-  constexpr int XCH = (D / 16) * 4 + 4;  // MT float4s + (max, sum) padded to a float4
+  constexpr int MT = D / 16;
   const int J = W / hkv;
   MfmaLds L;
   L.tiles = 0;
-  L.slots = W * 16 * D * 2;
-  L.meta = align_up(L.slots + (W - W / J) * XCH * 64 * 4, 16);
+  L.slots = W * 16 * D * 2;                 // (max, sum) pairs: W * 64 float2
+  L.copies = L.slots + W * 64 * 8;          // tile copies: [hkv][MT][J - 1][64] float4
+  L.meta = align_up(L.copies + hkv * (J - 1) * MT * 1024, 16);
   L.q = L.meta + align_up((2 * kMetaCap + 1) * 4, 16);
   L.total = L.q + (qseg + 1) * hq * D * 2;
   return L;
@@ -126,21 +129,25 @@ __host__ __device__ inline int mfma_qseg(int hq, int d) {
   return n < 1 ? 1 : (n > kQSegMax ? kQSegMax : n);
 }
 
-template <typename T, int D, int W>
+// J = W / hkv waves share each KV head (a template parameter: the combine's loops and
+// register arrays are sized by it).
+template <typename T, int D, int W, int J>
 __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
+  constexpr int NT = W * 64;
   constexpr int KSTEPS = D / 32;        // Q.K^T matrix steps (k = 32 dims each)
   constexpr int MT = D / 16;            // P.V output tiles of 16 dims
   constexpr int CPR = D / 8;            // 16-byte chunks per token row
   constexpr int VCH = 16 * CPR / 64;    // V chunks per lane per page
   constexpr int ROWB = D * 2;           // bytes per staged V row
   constexpr int TILEB = 16 * ROWB;      // bytes per staged V page
-  constexpr int XCH = MT * 4 + 4;       // floats per lane of a parked softmax state
 
   extern __shared__ __align__(16) char smem[];
   __shared__ int s_pid[kPidCap];
   __shared__ int s_split[kMaxSplit][3];  // deferred arrivals: sequence, w_lo, w_hi
-  __shared__ int s_last[kMaxSplit];
-  __shared__ int s_nsplit;
+  __shared__ int s_merge[kMaxSplit][3];  // merges owed after the arrivals
+  __shared__ int s_nmerge;
+  __shared__ int s_next[8];              // per KV head: next range page to hand out
+  __shared__ int s_bf, s_bl, s_nseg;     // the range's first / last sequence, segment count
   // readfirstlane: the wave index (and all derived from it) is wave-uniform, so page ids
   // and addresses that depend on it become scalar values.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -151,37 +158,92 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   const int qseg = mfma_qseg(P.hq, D);
   const MfmaLds L = mfma_lds<D, W>(hkv, P.hq, qseg);
   char* vtile = smem + L.tiles + wave * TILEB;
-  int* s_indptr = reinterpret_cast<int*>(smem + L.meta);  // [kMetaCap + 1]
-  int* s_lastlen = s_indptr + kMetaCap + 1;               // [kMetaCap]
-  const T* s_q = reinterpret_cast<const T*>(smem + L.q);  // [qseg][hq][D]
+  float2* s_ml = reinterpret_cast<float2*>(smem + L.slots);   // [W][64]
+  f4* s_copy = reinterpret_cast<f4*>(smem + L.copies);        // [hkv][MT][J - 1][64]
+  int* s_indptr = reinterpret_cast<int*>(smem + L.meta);      // [kMetaCap + 1]
+  int* s_lastlen = s_indptr + kMetaCap + 1;                   // [kMetaCap]
+  const T* s_q = reinterpret_cast<const T*>(smem + L.q);      // [qseg + 1][hq][D]
   T* s_qw = reinterpret_cast<T*>(smem + L.q);
 
-  const int J = W / hkv;                 // waves sharing one KV head (hkv <= W)
-  const int h = wave / J, j = wave % J;  // this wave's KV head and its rank among the J
-  const bool active = h < hkv;
-  // parked-state slot of a non-leader wave (j > 0)
-  float* myslot = reinterpret_cast<float*>(smem + L.slots) + (h * (J - 1) + (j - 1)) * XCH * 64;
+  // Heads are dealt round-robin (h = wave % hkv): waves of one SIMD differ in issue
+  // priority by age, and this gives every head the same mix of older and younger waves.
+  const int h = wave % hkv, j = wave / hkv;  // this wave's KV head and its rank among the J
+  const bool active = j < J;
+
+  const int N0 = P.num_ctas;
+  // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each
+  // XCD a run of consecutive ranges keeps a split sequence's partials on one L2.
+  const int w0 = (N0 % 8 == 0) ? (int)(blockIdx.x % 8) * (N0 / 8) + (int)(blockIdx.x / 8)
+                               : (int)blockIdx.x;
+  // The first range's page ids are requested together with round 1, assuming the page list
+  // holds exactly indptr[B] entries (kv_indices sized to the batch): the partition then
+  // depends on num_indices alone.  Round 1 confirms the guess, or they are read again.
+  static_assert(kPidCap <= 4 * NT, "four page ids per thread");
+  const int tg = (int)(P.num_indices < INT_MAX ? P.num_indices : INT_MAX);
+  int pv[4];
+  {
+    int gp0 = 0, glen = 1;
+    if (tg > 0) {
+      const int ng = decode_ranges(N0, tg);
+      if (w0 < ng) {
+        const Ranges rg(ng, tg);
+        gp0 = rg.start(w0);
+        glen = rg.start(w0 + 1) - gp0;
+      }
+    }
+    const int32_t* src = tg > 0 ? P.indices + gp0 : P.indptr;  // (a valid address either way)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // unconditional loads from clamped indices
+      const int t = threadIdx.x + r * NT;
+      pv[r] = src[tg > 0 ? (t < glen ? t : glen - 1) : 0];
+    }
+  }
 
   // ---- round 1: the page table's row pointers and last-page lengths into LDS
-  for (int i = threadIdx.x; i <= B; i += blockDim.x) s_indptr[i] = P.indptr[i];
-  for (int i = threadIdx.x; i < B; i += blockDim.x) s_lastlen[i] = P.last[i];
-  if (threadIdx.x == 0) s_nsplit = 0;
+  // (B <= kMetaCap <= 4 * NT).  The loads are unconditional, from clamped indices, and all
+  // are issued before the first LDS write: a load under a divergent branch gets a wait for
+  // its result at the branch's end, which would serialise them.
+  {
+    static_assert(kMetaCap <= 4 * NT, "four rows per thread");
+    int iv[5], lv[4];
+#pragma unroll
+    for (int r = 0; r < 5; ++r) {
+      const int i = threadIdx.x + r * NT;
+      iv[r] = P.indptr[i < B ? i : B];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = threadIdx.x + r * NT;
+      lv[r] = P.last[i < B - 1 ? i : B - 1];
+    }
+#pragma unroll
+    for (int r = 0; r < 5; ++r) {
+      const int i = threadIdx.x + r * NT;
+      if (i <= B) s_indptr[i] = iv[r];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = threadIdx.x + r * NT;
+      if (i < B) s_lastlen[i] = lv[r];
+    }
+  }
+  if (threadIdx.x == 0) {
+    s_nseg = 0;
+    s_bf = INT_MAX;
+    s_bl = -1;
+  }
   if (blockIdx.x == 0) zero_empty_sequences<T, D>(P);
   lds_barrier();
   auto rd = [&](const int* lds_arr, int i) __attribute__((always_inline)) -> int {  // uniform LDS read
     return __builtin_amdgcn_readfirstlane(lds_arr[i]);
   };
-  int64_t total = rd(s_indptr, B);
-  total = total < P.num_indices ? total : P.num_indices;
+  int total = rd(s_indptr, B);
+  total = (int64_t)total < P.num_indices ? total : (int)P.num_indices;
   if (total <= 0) return;
-  const int N0 = P.num_ctas;
   // Ranges: one per workgroup, never more than there are pages and never more than
   // kPidCap pages each (a workgroup then walks ranges w, w + N0, ...).
   const int N = decode_ranges(N0, total);
-  // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each
-  // XCD a run of consecutive ranges keeps a split sequence's partials on one L2.
-  const int w0 = (N0 % 8 == 0) ? (int)(blockIdx.x % 8) * (N0 / 8) + (int)(blockIdx.x / 8)
-                               : (int)blockIdx.x;
+  const Ranges R(N, total);
 
   const T* kc = reinterpret_cast<const T*>(P.k_cache);
   const T* vc = reinterpret_cast<const T*>(P.v_cache);
@@ -199,87 +261,150 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
     voff[r] = (uint32_t)((c / CPR) * rowstride + 8 * (c % CPR));
   }
 
-  // Deferred arrivals: bump the counters of the parked split segments in parallel, then
-  // merge the sequences this workgroup completed.
-  auto flush_splits = [&]() __attribute__((always_inline)) {
-    wait_stores();  // this thread's partial stores are complete (device-visible)
-    lds_barrier();
-    const int ns = s_nsplit;
-    if ((int)threadIdx.x < ns) {
-      const int sb = s_split[threadIdx.x][0];
-      const int nseg = s_split[threadIdx.x][2] - s_split[threadIdx.x][1] + 1;
-      const int old = atomicAdd(&P.counters[sb], 1);
-      const int last = old == nseg - 1;
-      if (last) __hip_atomic_store(&P.counters[sb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last[threadIdx.x] = last;
+  // Deferred arrivals (split segments recorded in s_split; the count is kept in a register
+  // in every wave, as whether a segment is split is the same in all of them): every wave
+  // waits for its own partial stores, then one lane per split bumps that sequence's counter
+  // (all in parallel); the splits that arrived last are compacted into s_merge and merged
+  // by the whole workgroup at once.  Inside the page loop (a full record) the register-light
+  // global-memory merge is used: the page buffers are live there.
+  int nsplit = 0;
+  auto flush_splits = [&](bool in_loop) __attribute__((always_inline)) {
+    wait_stores();  // this wave's partial stores are complete (device-visible)
+    lds_barrier();  // ... in every wave; the split records are visible
+    if (wave == 0) {
+      int sb = 0, lo = 0, hi = 0, last = 0;
+      if (lane < nsplit) {
+        sb = s_split[lane][0];
+        lo = s_split[lane][1];
+        hi = s_split[lane][2];
+        const int old = atomicAdd(&P.counters[sb], 1);
+        last = old == hi - lo;
+        // Every other arrival already happened: safe to reset for the next launch.
+        if (last) __hip_atomic_store(&P.counters[sb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      const uint64_t bal = __ballot(last);
+      if (last) {
+        const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+        s_merge[pos][0] = sb;
+        s_merge[pos][1] = lo;
+        s_merge[pos][2] = hi;
+      }
+      if (lane == 0) s_nmerge = __popcll(bal);
     }
     lds_barrier();  // also keeps partial loads below the arrivals
-    for (int i = 0; i < ns; ++i) {
-      if (!s_last[i]) continue;
-      const int sb = s_split[i][0], lo = s_split[i][1], hi = s_split[i][2];
-      if (hi - lo + 1 <= kMergeRegs)
-        merge_partials_regs<T, D>(P, sb, lo, hi);
-      else
-        merge_partials<T, D>(P, sb, lo, hi);
+    const int nm = __builtin_amdgcn_readfirstlane(s_nmerge);
+    if (in_loop) {
+      for (int i = 0; i < nm; ++i) merge_partials<T, D>(P, s_merge[i][0], s_merge[i][1], s_merge[i][2]);
+    } else {
+      merge_queued<T, D>(P, s_merge, nm);
     }
-    lds_barrier();
-    if (threadIdx.x == 0) s_nsplit = 0;
-    lds_barrier();
+    lds_barrier();  // s_split / s_merge are free again
+    nsplit = 0;
   };
 
   for (int w = w0; w < N; w += N0) {
-  const int64_t p0 = range_start(w, N, total), p1 = range_start(w + 1, N, total);
-  const int bf = lds_upper_index(s_indptr, B, p0);
-  // The range's first qseg sequences (with pages in the range), whose q rows get staged.
-  // (Named scalars, not an array: a dynamically indexed array would live in scratch.)
-  int qb0 = bf, qb1 = bf, qb2 = bf, qb3 = bf;
-  int nq = 0;
-  {
-    int bb = bf;
-    int64_t pp = p0;
-    while (pp < p1 && nq < qseg && bb < B) {
-      const int e = rd(s_indptr, bb + 1);
-      if (e > pp) {
-        qb0 = nq == 0 ? bb : qb0;
-        qb1 = nq == 1 ? bb : qb1;
-        qb2 = nq == 2 ? bb : qb2;
-        qb3 = nq == 3 ? bb : qb3;
-        ++nq;
-        pp = e < p1 ? e : p1;
-      }
-      ++bb;
+  const int64_t p0 = R.start(w), p1 = R.start(w + 1);
+  const int len = (int)(p1 - p0);
+  lds_barrier();  // the previous range's readers are done with s_pid / s_q / s_bf / s_bl
+
+  // ---- round 2: the range's page ids (requested at the start for the first range when
+  // the page list is exactly indptr[B] long; otherwise now), written to LDS below ...
+  if (w != w0 || total != tg) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // unconditional loads from clamped indices, as in round 1
+      const int t = threadIdx.x + r * NT;
+      pv[r] = P.indices[p0 + (t < len ? t : len - 1)];
     }
   }
-  // ---- round 2: the range's page ids and the staged q rows into LDS
-  lds_barrier();  // the previous range's readers are done with s_pid / s_q
-  for (int t = threadIdx.x; t < p1 - p0; t += blockDim.x)
-    s_pid[t] = (int)page_at(P.indices, p0 + t, P.num_pages);
-  {
-    const int per = P.hq * (D / 8);  // 16-byte chunks per sequence
-    for (int c = threadIdx.x; c < nq * per; c += blockDim.x) {
-      const int i = c / per, r = c - i * per;
-      const int hh = r / (D / 8), d = (r - hh * (D / 8)) * 8;
-      const int sb = i == 0 ? qb0 : i == 1 ? qb1 : i == 2 ? qb2 : qb3;
-      const T* src = qall + sb * P.q_sn + (int64_t)hh * P.q_sh + d;
-      T* dst = s_qw + ((int64_t)(i * P.hq + hh)) * D + d;
-      if (P.q_vec) {
-        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
-      } else {
-#pragma unroll
-        for (int x = 0; x < 8; ++x) dst[x] = src[x];
-      }
+  // ... while all threads look up the range's sequences in the staged rows: the first and
+  // last sequence with pages in [p0, p1) and how many have any (the segments).
+  for (int i = threadIdx.x; i < B; i += NT) {
+    const int64_t s = s_indptr[i], e = s_indptr[i + 1];
+    if (e > s && e > p0 && s < p1) {
+      atomicAdd(&s_nseg, 1);
+      atomicMin(&s_bf, i);
+      atomicMax(&s_bl, i);
     }
   }
   lds_barrier();
-
-  // The wave streams range pages p0 + j + J*k, k = 0..nk-1, across sequence boundaries.
-  const int64_t len = p1 - p0;
-  const int nk = (active && len > j) ? (int)((len - j + J - 1) / J) : 0;
-  auto pid_of = [&](int k) __attribute__((always_inline)) -> int {  // id of wave page k (clamped to the last one)
-    k = k < nk ? k : nk - 1;
-    return __builtin_amdgcn_readfirstlane(s_pid[j + J * k]);  // uniform: an SGPR
+  const int bf = rd(&s_bf, 0), nseg = rd(&s_nseg, 0);
+  if (nseg == 0) continue;  // pages before indptr[0]: no sequence owns them
+  const int nq = min(qseg, rd(&s_bl, 0) - bf + 1);  // sequences bf .. bf + nq - 1 get staged
+  const int per = P.hq * (D / 8);  // 16-byte q chunks per sequence
+  const int nqc = nq * per;        // <= 4 * NT: qseg * hq * D * 2 <= 32 KB
+  auto q_src = [&](int c) __attribute__((always_inline)) -> const T* {
+    const int i = c / per, rr = c - i * per;
+    const int hh = rr / (D / 8), d = (rr - hh * (D / 8)) * 8;
+    return qall + (bf + i) * P.q_sn + (int64_t)hh * P.q_sh + d;
   };
-  // A page id outside the pool is read as page 0; its tokens are masked (nv = 0).
+  auto write_pids = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // ids outside the pool are read as absent (-1)
+      const int t = threadIdx.x + r * NT;
+      if (t < len) s_pid[t] = ((int64_t)pv[r] >= 0 && (int64_t)pv[r] < P.num_pages) ? pv[r] : -1;
+    }
+  };
+  // Staged row i, head hh lives at s_q[(i * hq + hh) * D]: chunk c maps to c * 8.  When a
+  // thread stages at most one chunk (the common case) it is kept in a register and written
+  // after the first K/V loads are issued, so those do not wait for the q rows.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (a plain vector: stays in registers)
+  const bool q_one = P.q_vec && nqc <= NT;
+  const u32x4 qc0 = *reinterpret_cast<const u32x4*>(
+      q_one ? q_src((int)threadIdx.x < nqc ? (int)threadIdx.x : nqc - 1)
+            : reinterpret_cast<const T*>(P.part_o));  // (unconditional: any aligned address)
+  if (!q_one && P.q_vec) {
+    u32x4 qc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = threadIdx.x + r * NT;
+      qc[r] = *reinterpret_cast<const u32x4*>(q_src(c < nqc ? c : nqc - 1));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = threadIdx.x + r * NT;
+      if (c < nqc) *reinterpret_cast<u32x4*>(s_qw + (int64_t)c * 8) = qc[r];
+    }
+  } else if (!q_one) {
+    for (int c = threadIdx.x; c < nqc; c += NT) {
+      const T* src = q_src(c);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) s_qw[(int64_t)c * 8 + x] = src[x];
+    }
+  }
+  write_pids();
+  // Pages before the first sequence (only when indptr[0] > 0) are skipped.
+  const int gap0 = (int)max((int64_t)rd(s_indptr, bf) - p0, (int64_t)0);
+  if (threadIdx.x < 8) s_next[threadIdx.x] = gap0;
+  lds_barrier();
+  if (threadIdx.x == 0) {  // (read by every thread before the barrier above)
+    s_nseg = 0;
+    s_bf = INT_MAX;
+    s_bl = -1;
+  }
+
+  // The J waves of a head split the range's pages, each in increasing order: by default
+  // wave j takes pages j, j + J, j + 2J, ... (a fixed split: the result is reproducible);
+  // with P.dynamic the waves take them on demand from the head's LDS counter, so a wave
+  // that gets fewer issue slots takes fewer pages and the J waves finish together.
+  int next_static = gap0 + j;
+  auto grab = [&]() __attribute__((always_inline)) -> int {  // next page of this head (uniform)
+    if (P.dynamic) {
+      int v = 0;
+      if (lane == 0) v = atomicAdd(&s_next[h], 1);
+      return __builtin_amdgcn_readfirstlane(v);
+    }
+    const int v = next_static;
+    next_static += J;
+    return v;
+  };
+  auto pid_at = [&](int i) __attribute__((always_inline)) -> int {  // id of range page i (uniform)
+    return __builtin_amdgcn_readfirstlane(s_pid[i < len ? i : len - 1]);
+  };
+  // A page id outside the pool is read as page 0; its tokens are masked (nv = 0).  Past the
+  // range's end the last page is loaded again (an L2 hit, never used): loads that are always
+  // issued keep the compiler's count of loads in flight exact, so that using one buffer
+  // never waits for the other.
   auto load_page = [&](int pgid, uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH]) __attribute__((always_inline)) {
     const int pg = pgid < 0 ? 0 : pgid;
     const T* kb = kc + (int64_t)pg * P.page_stride + hoff;  // uniform base
@@ -294,19 +419,6 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   // ---- the range's pages, one loop per wave; sequence (segment) boundaries are crossed
   // inside it.  Every wave ends each segment of the range once and in order, so the
   // combine barriers match up even though waves reach them at different pages.
-  int nseg = 0;  // segments in the range
-  {
-    int bb = bf;
-    int64_t pp = p0;
-    while (pp < p1 && bb < B) {
-      const int e = rd(s_indptr, bb + 1);
-      if (e > pp) {
-        ++nseg;
-        pp = e < p1 ? e : p1;
-      }
-      ++bb;
-    }
-  }
   int b = bf - 1, si = -1;
   int s1 = 0, last_len = 0, w_lo = 0, w_hi = 0;
   int64_t seg_end = p0;
@@ -327,17 +439,16 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
     last_len = rd(s_lastlen, b);
     last_len = last_len < 0 ? 0 : (last_len > 16 ? 16 : last_len);
     seg_end = p1 < s1 ? p1 : s1;
-    w_lo = range_owner(s0, N, total);
-    w_hi = range_owner(s1 - 1, N, total);
+    w_lo = R.owner(s0);
+    w_hi = R.owner(s1 - 1);
     whole = w_lo == w_hi;
     // Q of this segment is read from LDS at every page (lane = head lr of the group,
-    // dims 32*s + 8*lg .. +7); a segment past the staged ones fills the spare slot first.
-    int qslot = si;
-    if (si >= nq) {
+    // dims 32*s + 8*lg .. +7); a sequence past the staged ones fills the spare slot first.
+    int qslot = b - bf;
+    if (qslot >= nq) {
       qslot = qseg;
       lds_barrier();  // the spare slot's previous readers are done
-      const int per = P.hq * (D / 8);
-      for (int c = threadIdx.x; c < per; c += blockDim.x) {
+      for (int c = threadIdx.x; c < per; c += NT) {
         const int hh = c / (D / 8), d = (c - hh * (D / 8)) * 8;
         const T* src = qall + b * P.q_sn + (int64_t)hh * P.q_sh + d;
         T* dst = s_qw + ((int64_t)(qseg * P.hq + hh)) * D + d;
@@ -354,41 +465,72 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   };
 
   auto end_segment = [&]() __attribute__((always_inline)) {  // uniform across the workgroup
-    // Combine the J waves of each head: non-leaders park their state, the leader (j == 0)
-    // folds it in and writes the output row or the split partial.
-    if (J > 1) {
-      if (active && j > 0) {
+    // Combine the J waves of each head, all of them at once: wave j owns the output tiles
+    // mt = j, j + J, ...  Every wave parks its (max, sum) and the tiles it does not own;
+    // then each wave folds the J copies of its own tiles.
+    if constexpr (J > 1) {
+      if (active) {
+        s_ml[(h * J + j) * 64 + lane] = make_float2(m, lsum);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          *reinterpret_cast<f4*>(myslot + (mt * 64 + lane) * 4) = o[mt];
-        *reinterpret_cast<float2*>(myslot + (MT * 64 + lane) * 4) = make_float2(m, lsum);
-      }
-      lds_barrier();
-      if (active && j == 0) {
-        for (int jj = 1; jj < J; ++jj) {
-          const float* xb = reinterpret_cast<const float*>(smem + L.slots) + (h * (J - 1) + (jj - 1)) * XCH * 64;
-          const float2 ml2 = *reinterpret_cast<const float2*>(xb + (MT * 64 + lane) * 4);
-          const float m2 = ml2.x, l2 = ml2.y;
-          const float mm = fmaxf(m, m2);
-          const float mu = mm == -INFINITY ? 0.f : mm;
-          const float c1 = __builtin_amdgcn_exp2f(m - mu), c2 = __builtin_amdgcn_exp2f(m2 - mu);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            o[mt] = o[mt] * c1 + *reinterpret_cast<const f4*>(xb + (mt * 64 + lane) * 4) * c2;
-          lsum = lsum * c1 + l2 * c2;
-          m = mm;
+        for (int mt = 0; mt < MT; ++mt) {
+          const int c = mt % J;
+          if (c != j) s_copy[((h * MT + mt) * (J - 1) + (j < c ? j : j - 1)) * 64 + lane] = o[mt];
         }
       }
+      lds_barrier();
+      if (active) {
+        float2 mls[J];
+#pragma unroll
+        for (int jj = 0; jj < J; ++jj) mls[jj] = s_ml[(h * J + jj) * 64 + lane];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int jj = 0; jj < J; ++jj) mx = fmaxf(mx, mls[jj].x);
+        const float mu = mx == -INFINITY ? 0.f : mx;
+        float sc[J];
+        float ls = 0.f, cj = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < J; ++jj) {
+          sc[jj] = __builtin_amdgcn_exp2f(mls[jj].x - mu);
+          ls += mls[jj].y * sc[jj];
+          cj = jj == j ? sc[jj] : cj;
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if (mt % J != j) continue;
+          f4 cp[J - 1];
+#pragma unroll
+          for (int jj = 0; jj < J - 1; ++jj) cp[jj] = s_copy[((h * MT + mt) * (J - 1) + jj) * 64 + lane];
+          f4 acc = o[mt] * cj;
+#pragma unroll
+          for (int jj = 0; jj < J - 1; ++jj) {
+            const int src = jj < j ? jj : jj + 1;  // wave rank that parked copy jj
+            float s2 = 0.f;
+#pragma unroll
+            for (int x = 0; x < J; ++x) s2 = x == src ? sc[x] : s2;
+            acc += cp[jj] * s2;
+          }
+          o[mt] = acc;
+        }
+        m = mx;
+        lsum = ls;
+      }
     }
+    if (!whole && threadIdx.x == 0) {
+      s_split[nsplit][0] = b;
+      s_split[nsplit][1] = w_lo;
+      s_split[nsplit][2] = w_hi;
+    }
+    lds_barrier();  // slots are read before the next segment parks new states
     float ltot = lsum + __shfl_xor(lsum, 16, 64);
     ltot += __shfl_xor(ltot, 32, 64);
-    if (active && j == 0 && lr < g) {
+    if (active && lr < g) {
       const int hq = h * g + lr;
       const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
       if (whole) {
         T* orow = out + b * P.o_sn + (int64_t)hq * P.o_sh + 4 * lg;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
+          if (mt % J != j) continue;
           if (P.o_vec) {
             const uint2 pk = make_uint2(Mma<T>::pack(o[mt][0] * inv, o[mt][1] * inv),
                                         Mma<T>::pack(o[mt][2] * inv, o[mt][3] * inv));
@@ -401,20 +543,14 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
       } else {
         const int64_t sidx = ((int64_t)w + b) * P.hq + hq;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt) {
+          if (mt % J != j) continue;
           st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), o[mt] * inv);
-        if (lg == 0) store_partial_ml(P, sidx, m, ltot);
+        }
+        if (j == 0 && lg == 0) store_partial_ml(P, sidx, m, ltot);
       }
     }
-    if (!whole && threadIdx.x == 0) {
-      const int n = s_nsplit;
-      s_split[n][0] = b;
-      s_split[n][1] = w_lo;
-      s_split[n][2] = w_hi;
-      s_nsplit = n + 1;
-    }
-    lds_barrier();  // slots are read before the next segment parks new states
-    if (s_nsplit == kMaxSplit) flush_splits();
+    if (!whole && ++nsplit == kMaxSplit) flush_splits(true);
   };
   auto advance = [&]() __attribute__((always_inline)) {
     end_segment();
@@ -480,39 +616,51 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
     __builtin_amdgcn_wave_barrier();
   };
 
-  // One step: consume wave page kk from its buffer (A for even kk, B for odd), refill that
-  // buffer with page kk + 2 (clamped to the last page), so two pages are always in flight.
-  auto step = [&](uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH], int kk) __attribute__((always_inline)) {
-    const int64_t gp = p0 + j + (int64_t)J * kk;
+  // One step: consume range page idx from its buffer, then take the head's next page and
+  // refill the same buffer with it, so two pages are in flight per wave.
+  auto step = [&](uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH], int& idx) __attribute__((always_inline)) {
+    const int64_t gp = p0 + idx;
     while (gp >= seg_end) advance();
-    process(kr, vr, gp, pid_of(kk));
-    load_page(pid_of(kk + 2), kr, vr);
+    process(kr, vr, gp, pid_at(idx));
+    idx = grab();
+    load_page(pid_at(idx), kr, vr);
     __builtin_amdgcn_sched_barrier(0);
   };
   start_segment();
-  // Ping-pong buffers: page k lives in A when k is even, B when odd; two pages in flight.
-  // Issued only now, after the scalar set-up: work between these loads and their first use
-  // risks a wait that drains them.
+  // Ping-pong buffers A and B.  A wave's pages come in increasing order (ia < ib < next ia
+  // ...), so the first one past the range ends the wave's loop.
   uint4 kA[KSTEPS], vA[VCH], kB[KSTEPS], vB[VCH];
-  if (nk > 0) {
-    load_page(pid_of(0), kA, vA);
-    load_page(pid_of(1), kB, vB);  // nk == 1 reloads page 0: harmless, keeps the pipeline uniform
+  int ia = len, ib = len;
+  if (active) {
+    ia = grab();
+    ib = grab();
   }
-  for (int k = 0; k < nk; k += 2) {
-    step(kA, vA, k);
-    if (k + 1 < nk) step(kB, vB, k + 1);
+  load_page(pid_at(ia), kA, vA);
+  load_page(pid_at(ib), kB, vB);
+  if (q_one && (int)threadIdx.x < nqc) *reinterpret_cast<u32x4*>(s_qw + (int64_t)threadIdx.x * 8) = qc0;
+  lds_barrier();  // the q rows are staged
+  while (ia < len) {
+    step(kA, vA, ia);
+    if (ib >= len) break;
+    step(kB, vB, ib);
   }
   while (si < nseg - 1) advance();
   end_segment();
   }  // ranges
-  if (s_nsplit > 0) flush_splits();
+  if (nsplit > 0) flush_splits(false);
 }
 
 template <typename T, int D>
 int launch_mfma(const DecodeParams& P, hipStream_t s) {
   constexpr int W = 8;
   const MfmaLds L = mfma_lds<D, W>(P.hkv, P.hq, mfma_qseg(P.hq, D));
-  hipLaunchKernelGGL((decode_mfma_kernel<T, D, W>), dim3(P.num_ctas), dim3(W * 64), L.total, s, P);
+  const dim3 grid(P.num_ctas), block(W * 64);
+  switch (W / P.hkv) {  // 1 <= hkv <= 8: J is 8, 4, 2 or 1
+    case 8: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 8>), grid, block, L.total, s, P); break;
+    case 4: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 4>), grid, block, L.total, s, P); break;
+    case 2: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 2>), grid, block, L.total, s, P); break;
+    default: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 1>), grid, block, L.total, s, P); break;
+  }
   return (int)hipGetLastError();
 }
 

@@ -118,12 +118,15 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams P) {
   __shared__ int flag;
 
   const int w = blockIdx.x;
-  const int64_t total = total_pages(P);
+  const int total = total_pages(P);
   if (w == 0) zero_empty_sequences<T, D>(P);
   if (total == 0) return;
   const int N = effective_ranges(P.num_ctas, total);
   if (w >= N) return;
-  int64_t p = range_start(w, N, total), end = range_start(w + 1, N, total);
+  const Ranges R(N, total);
+  int64_t p = R.start(w), end = R.start(w + 1);
+  const int64_t first = P.indptr[0];  // pages before indptr[0] belong to no sequence
+  if (p < first) p = first < end ? first : end;
   const int g = P.hq / P.hkv;
   const T* kc = reinterpret_cast<const T*>(P.k_cache);
   const T* vc = reinterpret_cast<const T*>(P.v_cache);
@@ -139,7 +142,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams P) {
     const int t0 = (int)(p - s0) * P.ps;
     int t1 = (int)(seg_end - s0) * P.ps;
     if (t1 > len) t1 = len;
-    const int w_lo = range_owner(s0, N, total), w_hi = range_owner(s1 - 1, N, total);
+    const int w_lo = R.owner(s0), w_hi = R.owner(s1 - 1);
     const bool whole = w_lo == w_hi;
     const int64_t slot = (int64_t)w + b;
 

@@ -49,6 +49,8 @@ def _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, ro
         raise NotImplementedError("in-kernel RoPE is not implemented")
 
 
+_DECODE_VALU, _DECODE_DYNAMIC = 1, 2  # pkv_batch_decode flags (include/pagedkv.h)
+
 class BatchDecodeWithPagedKVCacheWrapper:
     """Paged decode attention: one query token per sequence (FlashInfer contract)."""
 
@@ -79,9 +81,12 @@ class BatchDecodeWithPagedKVCacheWrapper:
              pos_encoding_mode: str = "NONE", window_left: int = -1, logits_soft_cap=None,
              q_data_type="float16", kv_data_type=None, data_type=None, sm_scale=None,
              rope_scale=None, rope_theta=None, non_blocking: bool = True,
-             num_ctas: int | None = None, **_unused) -> None:
-        """``num_ctas`` (an extension) fixes the number of workgroups that share the batch's
-        pages; by default one per compute unit for the matrix-core kernel."""
+             num_ctas: int | None = None, deterministic: bool = True, **_unused) -> None:
+        """Extensions: ``num_ctas`` fixes the number of workgroups that share the batch's
+        pages (by default one per compute unit for the matrix-core kernel);
+        ``deterministic=False`` lets the waves of a workgroup take pages on demand, which is
+        a little faster but makes the last bits of the result vary from call to call (with
+        the default the result is bitwise reproducible, as FlashInfer's is)."""
         _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, rope_theta)
         self._indptr = _i32(indptr, "indptr")
         self._indices = _i32(indices, "indices")
@@ -121,6 +126,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
             check(lib().pkv_decode_workspace_init(self._workspace.data_ptr(), self._batch,
                                                   stream_ptr(dev)), "decode plan")
             self._counters_ready = self._batch
+        self._flags = 0 if deterministic else _DECODE_DYNAMIC
         self._planned = True
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,
@@ -149,7 +155,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
             self._last.data_ptr(), self._batch,
             self._hq, self._hkv, self._d, self._ps, self._sm_scale, self._ctas,
             self._workspace.data_ptr(), self._workspace.numel() * self._workspace.element_size(),
-            out.data_ptr(), out.stride(0), out.stride(1), dtype_code(q.dtype), int(force_valu),
+            out.data_ptr(), out.stride(0), out.stride(1), dtype_code(q.dtype),
+            self._flags | (_DECODE_VALU if force_valu else 0),
             stream_ptr(q.device)), "BatchDecodeWithPagedKVCacheWrapper.run")
         return out
 

@@ -89,9 +89,15 @@ int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
  * seq_len_b = (npages_b - 1) * page_size + kv_last_page_len[b] tokens of sequence b, with
  * KV head h / (num_qo_heads / num_kv_heads); fp32 accumulation, output in `dtype`.  A
  * sequence with no tokens yields zeros.  num_ctas workgroups each stream an equal share of
- * the batch's pages; force_valu = 1 selects the vector-ALU kernel for cross-checks.  Page
- * ids outside [0, num_pages) and page-list entries past num_indices are never read (their
- * tokens are treated as absent). */
+ * the batch's pages.  flags: PKV_DECODE_VALU selects the vector-ALU kernel (cross-checks);
+ * PKV_DECODE_DYNAMIC lets the waves of a workgroup take pages on demand instead of in a
+ * fixed order (a little faster; the summation order, and so the last bits of the result,
+ * then vary from call to call).  Without it the result is bitwise reproducible for a given
+ * num_ctas.  Page ids outside [0, num_pages) and page-list entries past num_indices are
+ * never read (their tokens are treated as absent); pages before kv_indptr[0] belong to no
+ * sequence. */
+#define PKV_DECODE_VALU 1
+#define PKV_DECODE_DYNAMIC 2
 int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k_cache,
                      const void* v_cache, int64_t page_stride, int64_t num_pages,
                      const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
@@ -99,7 +105,7 @@ int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, cons
                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t page_size, float sm_scale, int32_t num_ctas, void* workspace,
                      int64_t workspace_bytes, void* out, int64_t o_stride_n, int64_t o_stride_h,
-                     int32_t dtype, int32_t force_valu, void* stream);
+                     int32_t dtype, int32_t flags, void* stream);
 
 /* BatchPrefillWithPagedKVCacheWrapper.run(q, paged_kv_cache) after
  * plan(qo_indptr, kv_indptr, kv_indices, kv_last_page_len, ..., causal=...)

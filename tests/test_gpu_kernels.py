@@ -41,11 +41,13 @@ def _append_dev(dv):
                               dv.indices, dv.indptr, dv.last)
 
 
-def _decode_dev(dv, q, force_valu=False, num_ctas=None, cache=None, indices=None):
+def _decode_dev(dv, q, force_valu=False, num_ctas=None, cache=None, indices=None,
+                deterministic=True):
     ws = torch.empty(128 << 20, dtype=torch.uint8, device=DEV)
     w = BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
     w.plan(dv.indptr, dv.indices if indices is None else indices, dv.last, dv.hq, dv.hkv, dv.d,
-           dv.ps, pos_encoding_mode="NONE", q_data_type=dv.dtype, num_ctas=num_ctas)
+           dv.ps, pos_encoding_mode="NONE", q_data_type=dv.dtype, num_ctas=num_ctas,
+           deterministic=deterministic)
     return w.run(q, dv.cache if cache is None else cache, force_valu=force_valu)
 
 
@@ -169,6 +171,12 @@ DECODE_CASES = {
     "llama31_8b_bf16_b16": lambda: workloads.llama31_8b_decode(batch=16, lo=100, hi=3000),
     "mha_fp16_d64": lambda: workloads.build_batch([5, 70, 300, 1], [1] * 4, 4, 4, 64, torch.float16, 21),
     "g16_bf16_d64": lambda: workloads.build_batch([50, 17, 900], [1] * 3, 16, 1, 64, torch.bfloat16, 22),
+    # one KV head at head_dim 128: eight waves share the head
+    "mqa_fp16_d128": lambda: workloads.build_batch([700, 33, 1200, 16], [1] * 4, 8, 1, 128, torch.float16, 23),
+    # three KV heads: two waves per head, two waves idle
+    "gqa3_bf16_d128": lambda: workloads.build_batch([90, 640, 5], [1] * 3, 12, 3, 128, torch.bfloat16, 24),
+    # two KV heads at head_dim 64: four waves per head
+    "gqa2_fp16_d64": lambda: workloads.build_batch([260, 31, 77, 1000], [1] * 4, 8, 2, 64, torch.float16, 25),
 }
 
 
@@ -185,6 +193,47 @@ def test_decode_matches_oracle(name, force_valu):
     ref = kv_ref.decode(wb.q.float().numpy(), vals, wb.indptr.numpy(), wb.indices.numpy(),
                         wb.last.numpy(), wb.ps)
     np.testing.assert_allclose(o.float().cpu().numpy(), ref, **TOL[wb.dtype])
+
+
+@pytest.mark.parametrize("name", [n for n in DECODE_CASES if "fp32" not in n])
+def test_decode_dynamic_pages_match_oracle(name):
+    # waves take pages on demand: same result within tolerance, any partition of the pages
+    wb = DECODE_CASES[name]()
+    dv = wb.to(DEV)
+    _append_dev(dv)
+    _, vals = _oracle_appended(wb)
+    ref = kv_ref.decode(wb.q.float().numpy(), vals, wb.indptr.numpy(), wb.indices.numpy(),
+                        wb.last.numpy(), wb.ps)
+    for ctas in (None, 7):
+        o = _decode_dev(dv, dv.q, num_ctas=ctas, deterministic=False)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(o.float().cpu().numpy(), ref, **TOL[wb.dtype])
+
+
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_decode_pages_before_first_sequence(force_valu):
+    # kv_indptr[0] > 0: the leading page-list entries belong to no sequence
+    wb = workloads.build_batch([40, 300, 17], [1] * 3, 16, 2, 128, torch.float16, 41)
+    dv = wb.to(DEV)
+    _append_dev(dv)
+    _, vals = _oracle_appended(wb)
+    ref = kv_ref.decode(wb.q.float().numpy(), vals, wb.indptr.numpy(), wb.indices.numpy(),
+                        wb.last.numpy(), wb.ps)
+    lead = 37
+    # valid pages holding other sequences' data: counting them would change the result
+    pick = torch.randint(0, wb.indices.numel(), (lead,), generator=torch.Generator().manual_seed(2))
+    junk = wb.indices[pick]
+    indices = torch.cat([junk, wb.indices]).to(DEV)
+    indptr = (wb.indptr + lead).to(DEV)
+    for ctas in (1, 5, 64):
+        ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+        w = BatchDecodeWithPagedKVCacheWrapper(ws)
+        w.plan(indptr, indices, dv.last, dv.hq, dv.hkv, dv.d, 16, q_data_type=dv.dtype,
+               num_ctas=ctas)
+        o = w.run(dv.q, dv.cache, force_valu=force_valu)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(o.float().cpu().numpy(), ref, **TOL[wb.dtype],
+                                   err_msg=f"num_ctas={ctas}")
 
 
 @pytest.mark.parametrize("ctas", [1, 3, 17, 256, 1000])
