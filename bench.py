@@ -17,6 +17,11 @@ Printed JSON line:
   cpu_baseline    the reference's CPU path (gather pages, then torch SDPA, in fp32) on this
                   host's cores, on the same batch
   ms_per_step     append + decode per step, over exactly --steps timed steps
+
+roofline.traffic is the decode kernel's HBM bytes per launch measured with hardware counters
+(rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over `bench.py --profile-launches N`, each
+scaled by the same counter's reading for a plain copy of known size run in the same
+process); it is read from profiles/decode_traffic.json, where those runs were recorded.
 """
 from __future__ import annotations
 
@@ -30,6 +35,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_traffic.json")
 
 
 def decode_bytes(wb) -> int:
@@ -44,6 +50,19 @@ def append_bytes(wb) -> int:
     es = wb.cache.element_size()
     nnz = wb.k_new.shape[0]
     return nnz * (4 * wb.hkv * wb.d * es + 12)
+
+
+def measured_traffic(wb, w):
+    """HBM bytes per decode launch from the committed counter runs, when they were taken on
+    this workload and kernel (None otherwise)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("decode_bytes") != decode_bytes(wb) or t.get("decode_ctas") != w._ctas:
+        return None
+    return t.get("traffic_bytes")
 
 
 def cpu_model() -> str:
@@ -127,6 +146,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle parity check")
     ap.add_argument("--ctas", type=int, default=None, help="decode workgroups (default: one per CU)")
+    ap.add_argument("--dynamic", action="store_true",
+                    help="waves take pages on demand (faster, not bitwise reproducible)")
+    ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
+                    help="for counter runs: N eager decode and append launches, then N plain "
+                         "copies of the decode's byte count (the counters' calibration), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -151,7 +175,7 @@ def main():
     ws = torch.empty(128 << 20, dtype=torch.uint8, device=dev)
     w = BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
     w.plan(dv.indptr, dv.indices, dv.last, wb.hq, wb.hkv, wb.d, wb.ps, pos_encoding_mode="NONE",
-           q_data_type=wb.dtype, num_ctas=args.ctas)
+           q_data_type=wb.dtype, num_ctas=args.ctas, deterministic=not args.dynamic)
     outs = [torch.empty_like(dv.q) for _ in range(NL)]
 
     def append(l):
@@ -161,6 +185,15 @@ def main():
     def decode(l):
         w.run(dv.q, kv[l], out=outs[l])
 
+    # the vector-ALU kernel on the same batch, for comparison (its own default: 2 workgroups
+    # per CU)
+    wv = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=dev), "NHD")
+    wv.plan(dv.indptr, dv.indices, dv.last, wb.hq, wb.hkv, wb.d, wb.ps, pos_encoding_mode="NONE",
+            q_data_type=wb.dtype, num_ctas=2 * w._ctas)
+
+    def decode_valu(l):
+        wv.run(dv.q, kv[l], out=outs[l], force_valu=True)
+
     # eager warm-up and parity on layer 0
     for l in range(NL):
         append(l)
@@ -168,6 +201,22 @@ def main():
     torch.cuda.synchronize()
     par = None if args.no_check else parity(wb, outs[0])
     print(f"bench: parity {par}", file=sys.stderr, flush=True)
+
+    if args.profile_launches:
+        n = args.profile_launches
+        for i in range(n):
+            append(i % NL)
+            decode(i % NL)
+        # plain copy of decode_bytes: reads and writes exactly that many bytes
+        nb = decode_bytes(wb) // 16 * 16
+        src = torch.empty(nb // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(n):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_launches": n, "decode_bytes": decode_bytes(wb), "copy_bytes": nb}),
+              flush=True)
+        return
 
     stream = torch.cuda.Stream(device=dev)
 
@@ -182,6 +231,7 @@ def main():
     REP = 8  # launches per layer inside the per-kernel timing graphs
     dec_graph = capture(lambda: [decode(l) for _ in range(REP) for l in range(NL)])
     app_graph = capture(lambda: [append(l) for _ in range(REP) for l in range(NL)])
+    valu_graph = capture(lambda: [decode_valu(l) for l in range(NL)])
     torch.cuda.synchronize()
 
     def timed(fn, n):
@@ -208,6 +258,8 @@ def main():
     t_dec = timed(lambda i: dec_graph.replay(), n_rep) / (n_rep * REP * NL)
     app_graph.replay()
     t_app = timed(lambda i: app_graph.replay(), n_rep) / (n_rep * REP * NL)
+    valu_graph.replay()
+    t_valu = timed(lambda i: valu_graph.replay(), 3) / (3 * NL)
     torch.cuda.synchronize()
 
     dbytes = decode_bytes(wb)
@@ -239,6 +291,7 @@ def main():
         },
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "decode_us": round(t_dec * 1e6, 3),
+        "decode_valu_us": round(t_valu * 1e6, 3),
         "decode_bytes": dbytes,
         "append_mtok_s": round(nnz / t_app / 1e6, 3),
         "append_us": round(t_app * 1e6, 3),
@@ -249,7 +302,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(wb, w),
         },
         "parity": par,
     }

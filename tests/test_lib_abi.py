@@ -52,3 +52,14 @@ def test_workspace_sizing_is_host_only():
     assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 64) == 1
     assert _lib.lib().pkv_decode_uses_mfma(2, 64, 32, 8, 4) == 0
     assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 4096) == 0
+
+
+def test_flashinfer_namespace_covers_reference_call_sites():
+    import ecahlang_amd.fi as flashinfer
+
+    for name in ("get_seq_lens", "get_batch_indices_positions", "BatchDecodeWithPagedKVCacheWrapper",
+                 "BatchPrefillWithPagedKVCacheWrapper"):
+        assert callable(getattr(flashinfer, name))
+    assert callable(flashinfer.page.append_paged_kv_cache)
+    with pytest.raises(AttributeError, match="paged-KV path only"):
+        flashinfer.sampling
