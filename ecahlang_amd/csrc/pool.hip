@@ -1,0 +1,100 @@
+// Device-side page pool of the KV cache manager (ecahlang/manager.py:56, 99-120, 187-212).
+//
+// The reference keeps the free pages in a Python list used as a stack (pop() from the end,
+// extend() in page order on free) and each sequence's pages in a Python list.  Here both
+// live in device memory:
+//   stack[max_blocks]         free page ids; the live part is stack[0 .. n_free)
+//   table[rows][stride]       page list of each sequence slot (one row per slot, plus a row
+//                             for the CUDA-graph padding pages)
+// The host keeps only counts (n_free, pages per sequence), so it can raise the reference's
+// exceptions before anything is touched and compute every stack position itself; the page
+// ids never leave the device.  Operations are queued on the host and applied here in one
+// launch, in their original order.
+//
+//   pkv_pool_apply   <- allocate / append_tokens / free / init_cuda_graph_buffers
+//   pkv_pool_gather  <- get_append_metadata / fill_cuda_graph_metadata (the page walk that
+//                       builds kv_indices, manager.py:124-133, 231-246)
+#include "common.h"
+#include "../../include/pagedkv.h"
+
+using namespace pkv;
+
+namespace {
+
+// One workgroup applies the operations in order (a pop may read stack slots that an earlier
+// push of the same batch wrote).  Operation i is ops[5i .. 5i+4] = {kind, row, pos, col, n}:
+//   kind 0, pop:  table[row][col + k] = stack[pos - 1 - k]   (k < n: the order of pop())
+//   kind 1, push: stack[pos + k] = table[row][col + k]       (the order of extend())
+// Operations that fall outside the stack or the table are skipped and counted in *err.
+__global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
+                                  int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err) {
+  __shared__ int32_t s_op[5];
+  for (int i = 0; i < n_ops; ++i) {
+    if (threadIdx.x < 5) s_op[threadIdx.x] = ops[5 * i + threadIdx.x];
+    __syncthreads();
+    const int kind = s_op[0], row = s_op[1], pos = s_op[2], col = s_op[3], n = s_op[4];
+    const bool ok = (kind == 0 || kind == 1) && row >= 0 && row < rows && col >= 0 && n >= 0 &&
+                    (int64_t)col + n <= stride &&
+                    (kind == 0 ? (pos - n >= 0 && pos <= stack_size) : (pos >= 0 && pos + n <= stack_size));
+    if (!ok) {
+      if (threadIdx.x == 0 && err) atomicAdd(err, 1);
+    } else {
+      int32_t* trow = table + (int64_t)row * stride + col;
+      for (int k = threadIdx.x; k < n; k += blockDim.x) {
+        if (kind == 0) trow[k] = stack[pos - 1 - k];
+        else stack[pos + k] = trow[k];
+      }
+    }
+    __syncthreads();  // this operation's writes are visible to the next one
+  }
+}
+
+// indices[indptr[b] + k] = table[desc[4b]][desc[4b+1] + k] for k < desc[4b+2]; one thread per
+// output entry finds its sequence by binary search over indptr.
+__global__ void pool_gather_kernel(const int32_t* table, int64_t stride, int32_t rows, const int32_t* desc,
+                                   const int32_t* indptr, int32_t batch, int32_t* indices,
+                                   int64_t num_indices, int32_t* err) {
+  const int64_t total = indptr[batch] < num_indices ? indptr[batch] : num_indices;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    int lo = 0, hi = batch;  // largest b with indptr[b] <= t
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (indptr[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int row = desc[4 * lo], col = desc[4 * lo + 1], n = desc[4 * lo + 2];
+    const int64_t k = t - indptr[lo];
+    if (row >= 0 && row < rows && k < n && col + k < stride) {
+      indices[t] = table[(int64_t)row * stride + col + k];
+    } else {
+      indices[t] = -1;
+      if (err) atomicAdd(err, 1);
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
+                              int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err,
+                              void* stream) {
+  if (n_ops < 0 || stack_size < 0 || stride <= 0 || rows <= 0) return kBadArg;
+  if (n_ops == 0) return kOk;
+  hipLaunchKernelGGL(pool_apply_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, stack, stack_size,
+                     table, stride, rows, ops, n_ops, err);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t rows, const int32_t* desc,
+                               const int32_t* indptr, int32_t batch, int32_t* indices,
+                               int64_t num_indices, int64_t max_total, int32_t* err, void* stream) {
+  if (batch < 0 || stride <= 0 || rows <= 0 || num_indices < 0 || max_total < 0) return kBadArg;
+  if (batch == 0 || max_total == 0) return kOk;
+  const int64_t n = max_total < num_indices ? max_total : num_indices;
+  const int threads = 256;
+  int64_t blocks = (n + threads - 1) / threads;
+  blocks = blocks < 1024 ? (blocks > 0 ? blocks : 1) : 1024;
+  hipLaunchKernelGGL(pool_gather_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream,
+                     table, stride, rows, desc, indptr, batch, indices, num_indices, err);
+  return (int)hipGetLastError();
+}

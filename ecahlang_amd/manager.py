@@ -1,0 +1,441 @@
+"""AutoKVCacheManager with a device-resident page pool (ecahlang/manager.py:13-280).
+
+Same constructor, methods, attribute names and exception messages as the reference, which
+``ecahlang/main.py`` calls by name.  What changes is where the page ids live:
+
+* The free-page stack and each sequence's page list are int32 tensors on the GPU
+  (``csrc/pool.hip``).  The host keeps counts only: free pages, pages and last-page length per
+  sequence, sequence slots.  So every check the reference makes (and its exceptions) happens
+  on the host before anything is mutated, and every stack position is known on the host
+  without reading the device.
+* allocate / append_tokens / free / init_cuda_graph_buffers queue their pops and pushes;
+  one ``pkv_pool_apply`` launch applies the queue, in order, before the page lists are next
+  read.  The page ids are exactly the reference's: LIFO pops from the end of the free list,
+  frees pushed back in page order.
+* get_append_metadata / fill_cuda_graph_metadata compute ``kv_indptr`` and
+  ``kv_last_page_len`` on the host in O(batch) from the counts and gather ``kv_indices`` on
+  the device (``pkv_pool_gather``).  The reference's per-page Python walk and blocking H2D
+  copies (manager.py:124-137, 231-253) become one asynchronous copy of O(batch) integers and
+  one kernel.  Nothing here synchronises the device except the attributes that hand page ids
+  back to Python (``free_blocks`` contents, ``batch_to_blocks``, ``padding_pages``), which
+  ``main.py`` reads only for ``len(free_blocks)``.
+
+One deliberate divergence, shared with the oracle (oracle/manager_ref.py): ``allocate(T)``
+with ``T % block_size == 0`` records ``block_size`` as the last page's length instead of 0
+(manager.py:106).  The reference's 0 makes ``get_seq_lens`` report ``T - block_size`` while
+``T`` tokens are held; ``strict_reference_q1=True`` restores it.
+
+The sampling helpers (init_sampling_buffers, fill_sampling_params,
+fill_cuda_graph_sampling_params, ``mask_penalty``) are outside the paged-KV path; they are
+kept, as plain tensor code, so that ``main.py`` finds the attributes it uses.
+"""
+from __future__ import annotations
+
+import math
+from typing import Iterable
+
+import torch
+
+from ._lib import check, lib, stream_ptr
+from .ops import append_paged_kv_cache, get_batch_indices_positions, get_seq_lens
+
+_POP, _PUSH = 0, 1
+
+
+def get_total_free_memory(index: int = 0) -> int:
+    """Free bytes of device ``index`` (the reference reads them through NVML, manager.py:7-11)."""
+    return torch.cuda.mem_get_info(index)[0]
+
+
+def _to_device(values: list, device: torch.device) -> torch.Tensor:
+    """int32 values to the device through a pinned buffer, asynchronously on the current
+    stream (the caching host allocator keeps the buffer until the copy has run)."""
+    host = torch.tensor(values, dtype=torch.int32).pin_memory()
+    return host.to(device, non_blocking=True)
+
+
+class _FreeBlocks:
+    """``manager.free_blocks``: its length is known on the host; its contents (the free-page
+    stack, bottom to top) are read from the device on demand."""
+
+    __slots__ = ("_m",)
+
+    def __init__(self, m: "AutoKVCacheManager"):
+        self._m = m
+
+    def __len__(self) -> int:
+        return self._m._n_free
+
+    def tolist(self) -> list:
+        m = self._m
+        m._flush()
+        return m._stack[: m._n_free].tolist()
+
+    def __iter__(self):
+        return iter(self.tolist())
+
+    def __getitem__(self, i):
+        return self.tolist()[i]
+
+    def __eq__(self, other):
+        return self.tolist() == list(other)
+
+    def __repr__(self) -> str:
+        return repr(self.tolist())
+
+
+class _Pages:
+    """The page list ``allocate`` returns, read from the device on first use (the pages the
+    sequence held when it was allocated)."""
+
+    __slots__ = ("_m", "_row", "_n", "_list")
+
+    def __init__(self, m: "AutoKVCacheManager", row: int, n: int):
+        self._m, self._row, self._n, self._list = m, row, n, None
+
+    def tolist(self) -> list:
+        if self._list is None:
+            self._m._flush()
+            self._list = self._m._table[self._row, : self._n].tolist() if self._n else []
+        return self._list
+
+    def __len__(self) -> int:
+        return self._n
+
+    def __iter__(self):
+        return iter(self.tolist())
+
+    def __getitem__(self, i):
+        return self.tolist()[i]
+
+    def __eq__(self, other):
+        return self.tolist() == list(other)
+
+    def __repr__(self) -> str:
+        return repr(self.tolist())
+
+
+class AutoKVCacheManager:
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, vocab_size: int = 10000,
+                 seq_lens: int = 128, block_size: int = 16, dtype: torch.dtype = torch.float16,
+                 layout: str = "NHD", total_gpu_mem_bytes: int | None = None,
+                 mem_utilization: float = 0.9, *, device=None, max_pages_per_seq: int = 512,
+                 strict_reference_q1: bool = False):
+        """manager.py:14-72.  Extensions (keyword-only): ``device`` (default: the current
+        CUDA device), ``max_pages_per_seq`` (initial width of the per-sequence page table; it
+        grows on demand) and ``strict_reference_q1`` (see the module docstring)."""
+        if layout.upper() != "NHD":
+            raise NotImplementedError("only the NHD cache layout is implemented (the reference uses NHD)")
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if self.device.type != "cuda":
+            raise ValueError("the page pool lives on a CUDA (HIP) device")
+        lib()  # no fallback: a missing library fails here, not at the first step
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.vocab_size = vocab_size
+        self.seq_lens = max(seq_lens, 128)
+        self.block_size = block_size
+        self.dtype = dtype
+        self.layout = layout.upper()
+        self.dtype_size = torch.tensor([], dtype=dtype).element_size()
+        self.strict_reference_q1 = strict_reference_q1
+        self.mask_penalty = torch.ones(self.seq_lens, vocab_size, dtype=dtype, device=self.device)
+
+        if total_gpu_mem_bytes is None:
+            total_gpu_mem_bytes = get_total_free_memory(self.device.index or 0)
+        usable_mem = int(total_gpu_mem_bytes * mem_utilization)
+        per_token_bytes = num_kv_heads * head_dim * self.dtype_size * 2
+        per_block_per_layer = block_size * per_token_bytes
+        self.max_blocks = usable_mem // (num_layers * per_block_per_layer)
+        self.kv_cache = torch.zeros((num_layers, self.max_blocks, 2, block_size, num_kv_heads, head_dim),
+                                    dtype=dtype, device=self.device)
+
+        # device pool: free-page stack (bottom = page 0) and one page-list row per sequence
+        # slot, plus a last row for the CUDA-graph padding pages
+        self._stack = torch.arange(self.max_blocks, dtype=torch.int32, device=self.device)
+        self._n_free = self.max_blocks
+        self._rows = self.seq_lens + 1
+        self._stride = max(1, min(max(self.max_blocks, 1), max_pages_per_seq))
+        self._table = torch.full((self._rows, self._stride), -1, dtype=torch.int32, device=self.device)
+        self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._ops: list = []
+        self._n_padding = 0
+
+        # host bookkeeping: counts only
+        self.free_seq_lens = list(range(self.seq_lens))
+        self._npages: dict = {}
+        self.batch_to_page_lengths: dict = {}
+        self.batch_to_total_tokens: dict = {}
+        self.batch_to_seq_len: dict = {}
+        self.prefill_layer_idx = 0
+        self.decode_layer_idx = 0
+
+        self.cuda_graph_mode = False
+        self._cg_kv_indices: dict = {}
+        self._cg_kv_indptr: dict = {}
+        self._cg_kv_last_page_len: dict = {}
+        self._cg_batch_indices: dict = {}
+        self._cg_positions: dict = {}
+        self._cg_append_indptr: dict = {}
+
+    # ------------------------------------------------------------------ device pool plumbing
+
+    def _ensure_stride(self, need: int) -> None:
+        if need <= self._stride:
+            return
+        new = max(need, 2 * self._stride)
+        table = torch.full((self._rows, new), -1, dtype=torch.int32, device=self.device)
+        table[:, : self._stride].copy_(self._table)
+        self._table, self._stride = table, new
+
+    def _flush(self) -> None:
+        """Apply the queued pops and pushes (one launch, in order, on the current stream)."""
+        if not self._ops:
+            return
+        flat = [x for op in self._ops for x in op]
+        ops = _to_device(flat, self.device)
+        check(lib().pkv_pool_apply(self._stack.data_ptr(), self.max_blocks, self._table.data_ptr(),
+                                   self._stride, self._rows, ops.data_ptr(), len(self._ops),
+                                   self._err.data_ptr(), stream_ptr(self.device)), "page pool update")
+        self._ops = []
+
+    def _gather(self, desc: list, counts: list, out_indices: torch.Tensor, extra: list) -> torch.Tensor:
+        """indptr = exclusive scan of counts; out_indices[indptr[b] + k] = table[desc...].
+        Returns the device copy of [indptr | extra] (one asynchronous H2D copy)."""
+        self._flush()
+        b = len(counts)
+        indptr = [0]
+        for c in counts:
+            indptr.append(indptr[-1] + c)
+        dev = _to_device(desc + indptr + extra, self.device)
+        d_desc, d_rest = dev[: 4 * b], dev[4 * b:]
+        if indptr[-1]:
+            check(lib().pkv_pool_gather(self._table.data_ptr(), self._stride, self._rows, d_desc.data_ptr(),
+                                        d_rest.data_ptr(), b, out_indices.data_ptr(), out_indices.numel(),
+                                        indptr[-1], self._err.data_ptr(), stream_ptr(self.device)),
+                  "page table gather")
+        return d_rest
+
+    def pool_errors(self) -> int:
+        """Operations or gathers the device had to skip (0 unless the host bookkeeping and the
+        device pool disagree); reading it synchronises."""
+        return int(self._err.item())
+
+    # ------------------------------------------------------------------ reference attributes
+
+    @property
+    def free_blocks(self) -> _FreeBlocks:
+        return _FreeBlocks(self)
+
+    @property
+    def batch_to_blocks(self) -> dict:
+        """Page lists by sequence, read back from the device (synchronises)."""
+        self._flush()
+        if not self._npages:
+            return {}
+        rows = self._table.cpu()
+        return {b: rows[self.batch_to_seq_len[b], :n].tolist() for b, n in self._npages.items()}
+
+    @property
+    def padding_pages(self) -> list:
+        self._flush()
+        return self._table[self._rows - 1, : self._n_padding].tolist() if self._n_padding else []
+
+    # ------------------------------------------------------------------ page pool (A3-A5)
+
+    def allocate(self, batch_id, total_tokens: int) -> _Pages:
+        """manager.py:99-112: pop ceil(T / block_size) pages, take a sequence slot."""
+        num_pages = math.ceil(total_tokens / self.block_size)
+        if self._n_free < num_pages:
+            raise RuntimeError("Not enough KV cache blocks available")
+        if not self.free_seq_lens:
+            raise IndexError("pop from empty list")
+        slot = self.free_seq_lens.pop()
+        self._ensure_stride(num_pages)
+        if num_pages:
+            self._ops.append((_POP, slot, self._n_free, 0, num_pages))
+            self._n_free -= num_pages
+        self._npages[batch_id] = num_pages
+        page_len = total_tokens % self.block_size
+        if page_len == 0 and total_tokens > 0 and not self.strict_reference_q1:
+            page_len = self.block_size
+        self.batch_to_page_lengths[batch_id] = page_len
+        self.batch_to_total_tokens[batch_id] = total_tokens
+        self.batch_to_seq_len[batch_id] = slot
+        self.mask_penalty[slot] = 1.0
+        return _Pages(self, slot, num_pages)
+
+    def free(self, batch_id) -> None:
+        """manager.py:114-120: push the pages back in page order, release the slot."""
+        n = self._npages.pop(batch_id, 0)
+        self.batch_to_page_lengths.pop(batch_id, None)
+        slot = self.batch_to_seq_len.pop(batch_id, None)
+        if n and slot is not None:
+            self._ops.append((_PUSH, slot, self._n_free, 0, n))
+            self._n_free += n
+        if slot is not None:
+            self.free_seq_lens.append(slot)
+
+    def append_tokens(self, batch_id, num_new_tokens: int) -> None:
+        """manager.py:187-205: a page is popped as soon as the last one fills (an empty
+        trailing page with last_page_len 0 is kept, as the reference does)."""
+        if batch_id not in self._npages:
+            raise ValueError(f"{batch_id} not allocated")
+        current_len = self.batch_to_page_lengths.get(batch_id, 0)
+        total_tokens = current_len + num_new_tokens
+        full_new_pages = total_tokens // self.block_size
+        remaining = total_tokens % self.block_size
+        if full_new_pages > self._n_free:
+            raise RuntimeError("Not enough free blocks to append tokens")
+        if full_new_pages:
+            col = self._npages[batch_id]
+            self._ensure_stride(col + full_new_pages)
+            self._ops.append((_POP, self.batch_to_seq_len[batch_id], self._n_free, col, full_new_pages))
+            self._n_free -= full_new_pages
+            self._npages[batch_id] = col + full_new_pages
+        self.batch_to_page_lengths[batch_id] = remaining
+
+    # ------------------------------------------------------------------ page tables (A6-A9)
+
+    def get_append_metadata(self, batch_ids: Iterable) -> tuple:
+        """manager.py:122-138: (kv_indices, kv_indptr, kv_last_page_len), int32 on the device."""
+        batch_ids = list(batch_ids)
+        desc, counts, last = [], [], []
+        for bid in batch_ids:
+            n = self._npages[bid]
+            desc += [self.batch_to_seq_len[bid], 0, n, 0]
+            counts.append(n)
+            last.append(self.batch_to_page_lengths[bid])
+        kv_indices = torch.empty(sum(counts), dtype=torch.int32, device=self.device)
+        rest = self._gather(desc, counts, kv_indices, last)
+        b = len(batch_ids)
+        return kv_indices, rest[: b + 1], rest[b + 1: 2 * b + 1]
+
+    def prepare_append_metadata(self, batch_ids, append_indptr: torch.Tensor, nnz=None) -> None:
+        """manager.py:140-151: the page table, seq_lens, and each appended token's sequence
+        and position, cached for every layer of the step.  ``nnz`` (an extension) is the
+        number of appended tokens; without it ``append_indptr[-1]`` is read back, a device
+        synchronisation, as in the reference."""
+        kv_indices, kv_indptr, kv_last_page_len = self.get_append_metadata(batch_ids)
+        seq_lens = get_seq_lens(kv_indptr, kv_last_page_len, self.block_size)
+        batch_indices, positions = get_batch_indices_positions(
+            append_indptr, seq_lens, append_indptr[-1] if nnz is None else nnz)
+        self._cached_kv_indices = kv_indices
+        self._cached_kv_indptr = kv_indptr
+        self._cached_kv_last_page_len = kv_last_page_len
+        self._cached_batch_indices = batch_indices
+        self._cached_positions = positions
+
+    def append_paged_kv_cache_cached(self, key, value, layer_idx: int) -> None:
+        """manager.py:153-165."""
+        append_paged_kv_cache(append_key=key, append_value=value,
+                              batch_indices=self._cached_batch_indices, positions=self._cached_positions,
+                              paged_kv_cache=self.kv_cache[layer_idx], kv_indices=self._cached_kv_indices,
+                              kv_indptr=self._cached_kv_indptr,
+                              kv_last_page_len=self._cached_kv_last_page_len, kv_layout=self.layout)
+
+    def append_paged_kv_cache(self, batch_ids, key, value, append_indptr, layer_idx: int, nnz=None) -> None:
+        """manager.py:167-185 (the uncached variant)."""
+        kv_indices, kv_indptr, kv_last_page_len = self.get_append_metadata(batch_ids)
+        seq_lens = get_seq_lens(kv_indptr, kv_last_page_len, self.block_size)
+        batch_indices, positions = get_batch_indices_positions(
+            append_indptr, seq_lens, append_indptr[-1] if nnz is None else nnz)
+        append_paged_kv_cache(append_key=key, append_value=value, batch_indices=batch_indices,
+                              positions=positions, paged_kv_cache=self.kv_cache[layer_idx],
+                              kv_indices=kv_indices, kv_indptr=kv_indptr,
+                              kv_last_page_len=kv_last_page_len, kv_layout=self.layout)
+
+    # ------------------------------------------------------------------ CUDA-graph buckets (A10-A12)
+
+    def init_cuda_graph_buffers(self, bucket_sizes) -> None:
+        """manager.py:207-226: reserve max(bucket) padding pages and the static per-bucket
+        buffers the captured step reads."""
+        max_bucket = max(bucket_sizes)
+        if self._n_free < max_bucket:
+            raise RuntimeError(f"Not enough free blocks for {max_bucket} padding pages")
+        self._ensure_stride(max_bucket)
+        self._ops.append((_POP, self._rows - 1, self._n_free, 0, max_bucket))
+        self._n_free -= max_bucket
+        self._n_padding = max_bucket
+        dev = self.device
+        self._cg_temperature, self._cg_top_k, self._cg_top_p = {}, {}, {}
+        for bs in bucket_sizes:
+            self._cg_kv_indices[bs] = torch.zeros(self.max_blocks, dtype=torch.int32, device=dev)
+            self._cg_kv_indptr[bs] = torch.zeros(bs + 1, dtype=torch.int32, device=dev)
+            self._cg_kv_last_page_len[bs] = torch.zeros(bs, dtype=torch.int32, device=dev)
+            self._cg_batch_indices[bs] = torch.arange(bs, dtype=torch.int32, device=dev)
+            self._cg_positions[bs] = torch.zeros(bs, dtype=torch.int32, device=dev)
+            self._cg_append_indptr[bs] = torch.arange(bs + 1, dtype=torch.int32, device=dev)
+            self._cg_temperature[bs] = torch.ones(bs, 1, dtype=torch.float32, device=dev)
+            self._cg_top_k[bs] = torch.full((bs,), self.vocab_size, dtype=torch.int32, device=dev)
+            self._cg_top_p[bs] = torch.ones(bs, dtype=torch.float32, device=dev)
+
+    def fill_cuda_graph_metadata(self, bucket_size: int, real_uuids) -> None:
+        """manager.py:228-253: the real sequences' page tables and the position of each one's
+        newest token, then ``bucket - n`` padding rows (one padding page, last_page_len 1,
+        position 0), written into the bucket's static buffers on the device."""
+        real_uuids = list(real_uuids)
+        desc, counts, last, positions = [], [], [], []
+        for uid in real_uuids:
+            n = self._npages[uid]
+            pl = self.batch_to_page_lengths[uid]
+            desc += [self.batch_to_seq_len[uid], 0, n, 0]
+            counts.append(n)
+            last.append(pl)
+            positions.append((n - 1) * self.block_size + pl - 1)
+        for i in range(bucket_size - len(real_uuids)):
+            if i >= self._n_padding:
+                raise IndexError("list index out of range")
+            desc += [self._rows - 1, i, 1, 0]
+            counts.append(1)
+            last.append(1)
+            positions.append(0)
+        if sum(counts) > self._cg_kv_indices[bucket_size].numel():
+            raise RuntimeError("page table larger than the bucket's kv_indices buffer")
+        rest = self._gather(desc, counts, self._cg_kv_indices[bucket_size], last + positions)
+        b = len(counts)
+        self._cg_kv_indptr[bucket_size].copy_(rest[: b + 1])
+        self._cg_kv_last_page_len[bucket_size].copy_(rest[b + 1: 2 * b + 1])
+        self._cg_positions[bucket_size].copy_(rest[2 * b + 1: 3 * b + 1])
+
+    def append_paged_kv_cache_cuda_graph(self, key, value, bucket_size: int, layer_idx: int) -> None:
+        """manager.py:270-280."""
+        append_paged_kv_cache(append_key=key, append_value=value,
+                              batch_indices=self._cg_batch_indices[bucket_size],
+                              positions=self._cg_positions[bucket_size],
+                              paged_kv_cache=self.kv_cache[layer_idx],
+                              kv_indices=self._cg_kv_indices[bucket_size],
+                              kv_indptr=self._cg_kv_indptr[bucket_size],
+                              kv_last_page_len=self._cg_kv_last_page_len[bucket_size],
+                              kv_layout=self.layout)
+
+    # ------------------------------------------------------------------ sampling buffers (outside the path)
+    # main.py reads sampling_{temperature,top_k,top_p}_gpu and the bucket's _cg_* copies of
+    # them (main.py:360, 375-378, 462, 477-479); they are kept so it finds them.  Each call
+    # stages its values in a fresh pinned buffer, so a queued copy never sees them change.
+
+    def init_sampling_buffers(self, max_batch_size: int) -> None:
+        dev = self.device
+        self.sampling_temperature_gpu = torch.ones(max_batch_size, 1, dtype=torch.float32, device=dev)
+        self.sampling_top_k_gpu = torch.full((max_batch_size,), self.vocab_size, dtype=torch.int32, device=dev)
+        self.sampling_top_p_gpu = torch.ones(max_batch_size, dtype=torch.float32, device=dev)
+
+    @staticmethod
+    def _stage(dst: torch.Tensor, values, n: int) -> None:
+        src = torch.as_tensor(values, dtype=dst.dtype).reshape(-1)[:n].pin_memory()
+        dst.reshape(-1)[:n].copy_(src, non_blocking=True)
+
+    def fill_sampling_params(self, n: int, temperatures, top_ks, top_ps) -> None:
+        self._stage(self.sampling_temperature_gpu, temperatures, n)
+        self._stage(self.sampling_top_k_gpu, top_ks, n)
+        self._stage(self.sampling_top_p_gpu, top_ps, n)
+
+    def fill_cuda_graph_sampling_params(self, bucket_size: int, n: int, temperatures, top_ks, top_ps) -> None:
+        t, k, p = self._cg_temperature[bucket_size], self._cg_top_k[bucket_size], self._cg_top_p[bucket_size]
+        t.fill_(1.0)  # padding rows keep neutral values
+        k.fill_(self.vocab_size)
+        p.fill_(1.0)
+        self._stage(t, temperatures, n)
+        self._stage(k, top_ks, n)
+        self._stage(p, top_ps, n)

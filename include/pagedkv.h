@@ -122,6 +122,27 @@ int pkv_batch_prefill_valu(const void* q, int64_t q_stride_n, int64_t q_stride_h
                            void* out, int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
                            void* stream);
 
+/* Page pool of AutoKVCacheManager (ecahlang/manager.py:56, 99-120, 187-212), device side.
+ * stack[0 .. n_free) holds the free page ids (the reference's free_blocks list: pop() takes
+ * the last entry, extend() appends in page order); table is rows x stride int32, one row of
+ * page ids per sequence slot.  Applies n_ops queued operations in order; operation i is
+ * ops[5i .. 5i+4] = {kind, row, pos, col, n}:
+ *   kind 0, pop  (allocate :104, append_tokens :201-203, init_cuda_graph_buffers :212):
+ *     table[row][col + k] = stack[pos - 1 - k] for k < n
+ *   kind 1, push (free :116): stack[pos + k] = table[row][col + k] for k < n
+ * Operations outside the stack or table are skipped and counted in *err (may be NULL). */
+int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
+                   int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err, void* stream);
+
+/* The page walk of get_append_metadata / fill_cuda_graph_metadata (ecahlang/manager.py:124-133,
+ * :231-246): kv_indices[indptr[b] + k] = table[desc[4b]][desc[4b+1] + k] for k < desc[4b+2],
+ * with indptr[batch+1] (the exclusive scan of the desc counts) already on the device.  At most
+ * min(max_total, num_indices) entries are written; entries with no source are set to -1 and
+ * counted in *err (may be NULL). */
+int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t rows, const int32_t* desc,
+                    const int32_t* indptr, int32_t batch, int32_t* kv_indices, int64_t num_indices,
+                    int64_t max_total, int32_t* err, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,205 @@
+"""Device page pool (ecahlang_amd.manager.AutoKVCacheManager) against the oracle's list
+restatement of the reference manager: page ids, page lengths and page tables bit-exact, the
+same exceptions with the pool untouched, and an end-to-end step (allocate, append through the
+cached metadata, decode) against the attention oracle."""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from ecahlang_amd.manager import AutoKVCacheManager
+from ecahlang_amd.wrappers import BatchDecodeWithPagedKVCacheWrapper
+from oracle import kv_ref
+from oracle.manager_ref import RefKVCacheManager
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _pool(pages, strict=False, stride=4, layers=1, hkv=1, d=64, dtype=torch.float16):
+    es = torch.tensor([], dtype=dtype).element_size()
+    per_page = 16 * hkv * d * es * 2
+    m = AutoKVCacheManager(layers, hkv, d, total_gpu_mem_bytes=pages * per_page * layers, mem_utilization=1.0,
+                           dtype=dtype, device=DEV, max_pages_per_seq=stride, strict_reference_q1=strict)
+    assert m.max_blocks == pages
+    return m
+
+
+def _same_state(dev, ref):
+    assert list(dev.free_blocks) == ref.free_blocks
+    assert len(dev.free_blocks) == len(ref.free_blocks)
+    assert dev.batch_to_blocks == ref.batch_to_blocks
+    assert dev.batch_to_page_lengths == ref.batch_to_page_lengths
+    assert dev.batch_to_seq_len == ref.batch_to_seq_len
+    assert dev.free_seq_lens == ref.free_seq_lens
+
+
+def _run_trace(trace, strict):
+    m = _pool(trace["pool"], strict)
+    for op in trace["ops"]:
+        if strict and op.get("product_only"):
+            break
+        kind = op["op"]
+        if "error" in op:
+            exc = {"RuntimeError": RuntimeError, "ValueError": ValueError}[op["error"]]
+            before = list(m.free_blocks)
+            with pytest.raises(exc, match=op["message"]):
+                getattr(m, kind)(op["id"], op["n"])
+            assert list(m.free_blocks) == before
+            if "free_blocks" in op:
+                assert list(m.free_blocks) == op["free_blocks"]
+            continue
+        if kind in ("allocate", "append_tokens"):
+            got = getattr(m, kind)(op["id"], op["n"])
+            pages = op.get("reference_pages", op["pages"]) if strict else op["pages"]
+            plen = op.get("reference_page_len", op["page_len"]) if strict else op["page_len"]
+            if kind == "allocate":
+                assert list(got) == pages
+            assert m.batch_to_blocks[op["id"]] == pages, (trace["name"], op)
+            assert m.batch_to_page_lengths[op["id"]] == plen, (trace["name"], op)
+        elif kind == "free":
+            m.free(op["id"])
+            assert list(m.free_blocks) == op["free_blocks"], (trace["name"], op)
+        elif kind == "init_cuda_graph_buffers":
+            m.init_cuda_graph_buffers(op["buckets"])
+            assert m.padding_pages == op["padding_pages"]
+        elif kind == "fill_cuda_graph_metadata":
+            b = op["bucket"]
+            m.fill_cuda_graph_metadata(b, op["ids"])
+            n = len(op["kv_indices"])
+            assert m._cg_kv_indices[b][:n].tolist() == op["kv_indices"]
+            assert m._cg_kv_indptr[b].tolist() == op["kv_indptr"]
+            assert m._cg_kv_last_page_len[b].tolist() == op["kv_last_page_len"]
+            assert m._cg_positions[b].tolist() == op["positions"]
+        elif kind == "get_append_metadata":
+            idx, ptr, last = m.get_append_metadata(op["ids"])
+            assert (idx.tolist(), ptr.tolist(), last.tolist()) == (
+                op["kv_indices"], op["kv_indptr"], op["kv_last_page_len"])
+        else:
+            raise AssertionError(kind)
+    assert m.pool_errors() == 0
+
+
+@pytest.mark.parametrize("strict", [False, True])
+def test_hand_traces(golden, strict):
+    for trace in golden("manager_traces.json")["traces"]:
+        print(f"trace {trace['name']} strict={strict}", flush=True)
+        _run_trace(trace, strict)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_operations_match_oracle(seed):
+    # small pages-per-row start (stride 4) so page-table growth is exercised too
+    rng = random.Random(seed)
+    P = 60
+    dev, ref = _pool(P), RefKVCacheManager(P)
+    ids = list(range(8))
+    for step in range(250):
+        kind = rng.choice(["alloc", "alloc", "append", "append", "append", "free", "meta"])
+        sid = rng.choice(ids)
+        n = rng.choice([0, 1, 1, 1, 2, 15, 16, 17, 31, 33, 70])
+        if kind == "alloc" and sid not in ref.batch_to_blocks:
+            calls = ("allocate", (sid, n))
+        elif kind == "append" and sid in ref.batch_to_blocks:
+            calls = ("append_tokens", (sid, n))
+        elif kind == "append":
+            calls = ("append_tokens", (sid, n))  # unknown id: ValueError in both
+        elif kind == "free":
+            calls = ("free", (sid,))
+        else:
+            live = [s for s in ids if s in ref.batch_to_blocks]
+            rng.shuffle(live)
+            idx, ptr, last = dev.get_append_metadata(live)
+            assert (idx.tolist(), ptr.tolist(), last.tolist()) == tuple(map(list, ref.get_append_metadata(live)))
+            continue
+        name, args = calls
+        err_ref = err_dev = None
+        try:
+            getattr(ref, name)(*args)
+        except (RuntimeError, ValueError) as e:
+            err_ref = (type(e), str(e))
+        try:
+            getattr(dev, name)(*args)
+        except (RuntimeError, ValueError) as e:
+            err_dev = (type(e), str(e))
+        assert err_dev == err_ref, (step, name, args)
+        if step % 10 == 0 or err_ref:
+            _same_state(dev, ref)
+    _same_state(dev, ref)
+    assert dev.pool_errors() == 0
+
+
+def test_graph_buckets_match_oracle():
+    P = 200
+    dev, ref = _pool(P), RefKVCacheManager(P)
+    for m in (dev, ref):
+        m.init_cuda_graph_buffers([1, 2, 4, 8])
+    assert dev.padding_pages == ref.padding_pages
+    for i, t in enumerate([5, 16, 33, 100, 1]):
+        dev.allocate(i, t)
+        ref.allocate(i, t)
+    for i in range(5):
+        dev.append_tokens(i, 1)
+        ref.append_tokens(i, 1)
+    for bucket, real in ((8, [3, 0, 4, 1, 2]), (4, [2, 1]), (1, [4])):
+        dev.fill_cuda_graph_metadata(bucket, real)
+        idx, ptr, last, pos = ref.fill_cuda_graph_metadata(bucket, real)
+        assert dev._cg_kv_indices[bucket][: len(idx)].tolist() == idx
+        assert dev._cg_kv_indptr[bucket].tolist() == ptr
+        assert dev._cg_kv_last_page_len[bucket].tolist() == last
+        assert dev._cg_positions[bucket].tolist() == pos
+    with pytest.raises(RuntimeError, match="Not enough free blocks for 400 padding pages"):
+        dev.init_cuda_graph_buffers([400])
+    assert dev.pool_errors() == 0
+
+
+def test_end_to_end_prefill_then_decode_steps():
+    """allocate -> prepare_append_metadata -> cached append per layer -> decode plan/run,
+    for a prefill and three decode steps; every step checked against the oracle on the K/V
+    the test appended (tracked on the host)."""
+    L, hkv, hq, d, dt = 2, 2, 16, 128, torch.float16
+    P = 400
+    m = _pool(P, layers=L, hkv=hkv, d=d, stride=8)
+    gen = torch.Generator().manual_seed(11)
+    lens = [40, 1, 16, 250, 97]
+    ids = [f"r{i}" for i in range(len(lens))]
+    hist = {i: [[], []] for i in ids}  # per sequence: K rows, V rows (per layer stacked)
+
+    def append_step(new):  # new: tokens per sequence this step
+        append_indptr = torch.tensor(np.concatenate([[0], np.cumsum(new)]), dtype=torch.int32, device=DEV)
+        m.prepare_append_metadata(ids, append_indptr)
+        nnz = int(sum(new))
+        k = (torch.randn(L, nnz, hkv, d, generator=gen) * 0.5).to(dt)
+        v = (torch.randn(L, nnz, hkv, d, generator=gen) * 0.5).to(dt)
+        for layer in range(L):
+            m.append_paged_kv_cache_cached(k[layer].to(DEV), v[layer].to(DEV), layer)
+        off = 0
+        for sid, n in zip(ids, new):
+            hist[sid][0].append(k[:, off:off + n])
+            hist[sid][1].append(v[:, off:off + n])
+            off += n
+
+    for sid, n in zip(ids, lens):
+        m.allocate(sid, n)
+    append_step(lens)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    w = BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    for step in range(4):
+        if step:
+            for sid in ids:
+                m.append_tokens(sid, 1)
+            append_step([1] * len(ids))
+        w.plan(m._cached_kv_indptr, m._cached_kv_indices, m._cached_kv_last_page_len, hq, hkv, d, 16,
+               pos_encoding_mode="NONE", q_data_type=dt)
+        q = (torch.randn(len(ids), hq, d, generator=gen) * 0.5).to(dt)
+        for layer in range(L):
+            out = w.run(q.to(DEV), m.kv_cache[layer]).float().cpu().numpy()
+            for b, sid in enumerate(ids):
+                kk = torch.cat(hist[sid][0], 1)[layer].float().numpy()  # [len, hkv, d]
+                vv = torch.cat(hist[sid][1], 1)[layer].float().numpy()
+                ref = kv_ref._attend(q[b:b + 1].float().numpy().astype(np.float64), kk, vv,
+                                     [kk.shape[0]], d ** -0.5)[0]
+                np.testing.assert_allclose(out[b], ref, atol=2e-3, rtol=1e-2,
+                                           err_msg=f"step {step} layer {layer} seq {sid}")
+    assert m.pool_errors() == 0
