@@ -63,3 +63,12 @@ def test_flashinfer_namespace_covers_reference_call_sites():
     assert callable(flashinfer.page.append_paged_kv_cache)
     with pytest.raises(AttributeError, match="paged-KV path only"):
         flashinfer.sampling
+
+
+def test_attention_hook_registers_with_transformers():
+    from transformers import AttentionInterface
+
+    from ecahlang_amd import hook
+
+    hook.register()
+    assert AttentionInterface._global_mapping.get(hook.HOOK_NAME) is hook.ecah_attention
