@@ -139,3 +139,69 @@ def llama31_8b_decode(seed=1004, batch=128, lo=1024, hi=32768, pool_pages=None) 
     ctx = torch.floor(torch.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))).long().tolist()
     return build_batch([c + 1 for c in ctx], [1] * batch, 32, 8, 128, torch.bfloat16, seed,
                        scale=1.0, pool_pages=pool_pages)
+
+
+@dataclass
+class DeviceDecodeBatch:
+    """A decode batch generated directly in device memory (pools too large to build on the
+    host): the page table is built on the host, the K/V values with a device generator."""
+    hq: int
+    hkv: int
+    d: int
+    ps: int
+    dtype: torch.dtype
+    num_pages: int
+    kv_len: list
+    cache: torch.Tensor      # [P, 2, ps, Hkv, D] on the device, unused slots NaN
+    indptr: torch.Tensor     # device int32
+    indices: torch.Tensor
+    last: torch.Tensor
+    q: torch.Tensor          # [B, Hq, D] on the device
+
+    @property
+    def batch(self) -> int:
+        return len(self.kv_len)
+
+
+def device_decode_batch(kv_len, hq, hkv, d, dtype, seed, pool_pages, device, *, ps=16,
+                        scale=1.0) -> DeviceDecodeBatch:
+    """Pages of each sequence scattered by a seeded permutation of the pool (host); the used
+    pages filled with N(0,1)*scale on the device, every other slot (unused pages and the
+    slots past each sequence's last token) NaN."""
+    gen = torch.Generator().manual_seed(seed)
+    kv_len = [int(x) for x in kv_len]
+    npages = [(L + ps - 1) // ps for L in kv_len]
+    total = sum(npages)
+    if pool_pages < total:
+        raise ValueError("pool smaller than the pages the batch needs")
+    indices = torch.randperm(pool_pages, generator=gen)[:total].to(torch.int32)
+    indptr = torch.zeros(len(kv_len) + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(npages, dtype=torch.int64), 0).to(torch.int32)
+    last = torch.tensor([((L - 1) % ps) + 1 if L > 0 else 0 for L in kv_len], dtype=torch.int32)
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    cache = torch.full((pool_pages, 2, ps, hkv, d), float("nan"), dtype=dtype, device=device)
+    idx = indices.to(device).long()
+    chunk = 8192  # pages per fill (bounded temporary)
+    for s in range(0, total, chunk):
+        pg = idx[s:s + chunk]
+        cache[pg] = (torch.randn((pg.numel(), 2, ps, hkv, d), generator=dgen, device=device,
+                                 dtype=torch.float32) * scale).to(dtype)
+    for b, L in enumerate(kv_len):  # poison the tail of each last page
+        if L and last[b] < ps:
+            cache[int(indices[indptr[b + 1] - 1]), :, int(last[b]):] = float("nan")
+    q = (torch.randn((len(kv_len), hq, d), generator=dgen, device=device, dtype=torch.float32)
+         * scale).to(dtype)
+    return DeviceDecodeBatch(hq, hkv, d, ps, dtype, pool_pages, kv_len, cache, indptr.to(device),
+                             indices.to(device), last.to(device), q)
+
+
+def llama31_8b_decode_device(device, seed=1004, batch=128, lo=1024, hi=32768,
+                             pool_bytes=20_000_000_000) -> DeviceDecodeBatch:
+    """Long-context decode at Llama-3.1-8B shape (32 q / 8 kv heads, head_dim 128, bf16):
+    context log-uniform in [lo, hi], pages scattered over a pool of ~pool_bytes."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    u = torch.rand(batch, generator=g, dtype=torch.float64)
+    ctx = torch.floor(torch.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))).long().tolist()
+    page_bytes = 2 * 16 * 8 * 128 * 2
+    return device_decode_batch([c + 1 for c in ctx], 32, 8, 128, torch.bfloat16, seed,
+                               pool_bytes // page_bytes, device)
