@@ -143,6 +143,90 @@ def long_context(args, torch, workloads, Wrapper, dev):
     print(json.dumps(result), flush=True)
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+
+
+def chunked_prefill(args, torch, workloads, ops, dev):
+    """Chunked prefill at Qwen2.5-3B shape: append each request's chunk, then causal ragged
+    attention over prefix + chunk.  FLOPs count valid causal (query, key) pairs only:
+    4 * Hq * D * sum_b (C * P_b + C (C + 1) / 2)."""
+    import numpy as np
+    from ecahlang_amd.wrappers import BatchPrefillWithPagedKVCacheWrapper
+    print("bench: building Qwen2.5-3B chunked-prefill batch", file=sys.stderr, flush=True)
+    wb = workloads.qwen25_3b_prefill()
+    dv = wb.to(dev)
+    ops.append_paged_kv_cache(dv.k_new, dv.v_new, dv.batch_indices, dv.positions, dv.cache, dv.indices,
+                              dv.indptr, dv.last)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w.plan(dv.append_indptr, dv.indptr, dv.indices, dv.last, wb.hq, wb.hkv, wb.d, wb.ps, causal=True,
+           q_data_type=wb.dtype)
+    out = torch.empty_like(dv.q)
+    stream = torch.cuda.Stream(device=dev)
+
+    def timed_graph(fn, reps, n):
+        with torch.cuda.stream(stream):
+            fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for _ in range(reps):
+                    fn()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(n):
+                g.replay()
+            e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / (reps * n)
+
+    t = timed_graph(lambda: w.run(dv.q, dv.cache, out=out), 10, max(1, args.steps // 10))
+    t_valu = timed_graph(lambda: w.run(dv.q, dv.cache, out=out, force_valu=True), 1, 2)
+    C = wb.new_len[0]
+    prefix = [L - n for L, n in zip(wb.kv_len, wb.new_len)]
+    flops = 4 * wb.hq * wb.d * sum(C * p + C * (C + 1) // 2 for p in prefix)
+    tfs = flops / t / 1e12
+    # CPU baseline on a bounded sample (the reference's CPU path: gather, then causal SDPA with
+    # the bottom-right offset, fp32) for the shortest request
+    import torch.nn.functional as F
+    from oracle import kv_ref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    b = int(np.argmin(wb.kv_len))
+    qo = wb.append_indptr.tolist()
+    sample_q = wb.q[qo[b]:qo[b + 1]]
+    kk, vv = kv_ref.gather(wb.cache.numpy() if wb.dtype == torch.float32 else wb.cache.float().numpy(),
+                           wb.indices.numpy(), wb.indptr.numpy(), wb.last.numpy(), b, wb.ps)
+    kk, vv = torch.from_numpy(kk).float(), torch.from_numpy(vv).float()
+    L, qn = kk.shape[0], sample_q.shape[0]
+    mask = torch.arange(L)[None, :] <= (torch.arange(qn)[:, None] + L - qn)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        F.scaled_dot_product_attention(sample_q.float().transpose(0, 1)[None], kk.transpose(0, 1)[None],
+                                       vv.transpose(0, 1)[None], attn_mask=mask, enable_gqa=True)
+        times.append(time.perf_counter() - t0)
+    sample_flops = 4 * wb.hq * wb.d * (C * prefix[b] + C * (C + 1) // 2)
+    result = {
+        "metric": "chunked prefill attn TFLOP/s (% MFMA peak), Qwen2.5-3B 8 x 512-token chunks",
+        "value": round(tfs, 2), "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "fp16", "data": "synthetic (seeded N(0,1)*0.5, random page permutation, NaN-poisoned pool)",
+        "config": {"workload": "qwen2.5-3b chunked prefill, 1 layer, 8 requests x 512-token chunk onto prefix "
+                               "U[0,8192], causal, page 16, 16 q / 2 kv heads, head_dim 128, fp16",
+                   "requests": wb.batch, "q_rows": int(wb.q.shape[0]), "kv_tokens": sum(wb.kv_len),
+                   "work_items": w._n_items, "split_groups": w._n_groups, "chunk_keys": w._chunk},
+        "prefill_us": round(t * 1e6, 3), "prefill_valu_us": round(t_valu * 1e6, 3), "flops": flops,
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tfs / MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(sample_flops / statistics.median(times) / 1e12, 5), "unit": "TFLOP/s",
+                         "cores": cores, "kind": "port",
+                         "sample": f"request {b} ({qn} query rows over {L} keys): gather + fp32 causal SDPA, median of 3",
+                         "cpu_model": cpu_model()},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -226,10 +310,11 @@ def main():
     ap.add_argument("--ctas", type=int, default=None, help="decode workgroups (default: one per CU)")
     ap.add_argument("--dynamic", action="store_true",
                     help="waves take pages on demand (faster, not bitwise reproducible)")
-    ap.add_argument("--workload", default="qwen25_3b_b64", choices=["qwen25_3b_b64", "llama31_8b_b128"],
+    ap.add_argument("--workload", default="qwen25_3b_b64", choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill"],
                     help="qwen25_3b_b64: the headline decode + append step (default); llama31_8b_b128: "
                          "long-context decode at Llama-3.1-8B shape, B=128, ~4.4 GB of K/V in a 20 GB pool "
-                         "(decode only, generated on the device)")
+                         "(decode only, generated on the device); qwen25_3b_prefill: chunked prefill, 8 "
+                         "requests x 512-token chunks onto prefixes U[0, 8192] (the matrix-core roofline)")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="for counter runs: N eager decode and append launches, then N plain "
                          "copies of the decode's byte count (the counters' calibration), then exit")
@@ -248,6 +333,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "llama31_8b_b128":
         return long_context(args, torch, workloads, BatchDecodeWithPagedKVCacheWrapper, dev)
+    if args.workload == "qwen25_3b_prefill":
+        return chunked_prefill(args, torch, workloads, ops, dev)
     print("bench: building Qwen2.5-3B B=64 decode batch", file=sys.stderr, flush=True)
     wb = workloads.qwen25_3b_decode()
     NL = args.layers

@@ -37,6 +37,12 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32,
          _f32, _i32, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp],
     ),
+    "pkv_prefill_mfma_supported": (_i32, [_i32, _i32, _i32, _i32, _i32]),
+    "pkv_batch_prefill_mfma": (
+        _i32,
+        [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
+         _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    ),
     "pkv_pool_apply": (_i32, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _vp, _vp]),
     "pkv_pool_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _vp, _vp]),
     "pkv_batch_prefill_valu": (

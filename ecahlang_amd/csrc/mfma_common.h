@@ -1,0 +1,78 @@
+// Matrix-core building blocks shared by the paged decode and prefill kernels (gfx950).
+//
+//   Mma<T>::qk   v_mfma_f32_16x16x32_{f16,bf16}: 16x16 fp32 tile += A (16 x 32) * B (32 x 16);
+//                lane l supplies row/column l % 16, reduction elements 8*(l/16) .. +7
+//   Mma<T>::pv   v_mfma_f32_16x16x16{f16,bf16_1k}: reduction elements 4*(l/16) .. +3
+//   Accumulator layout (both): lane l holds C[4*(l/16) + i][l % 16], i = 0..3.
+//   lds_read_tr16 + vswz: the V^T operand of the P.V product read straight from a row-major,
+//   XOR-swizzled LDS copy of 16 value rows.
+#pragma once
+#include "common.h"
+
+namespace pkv {
+namespace mfma {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <typename To, typename From>
+__device__ __forceinline__ To bitcast_(const From& x) {
+  static_assert(sizeof(To) == sizeof(From), "size");
+  To y;
+  __builtin_memcpy(&y, &x, sizeof(To));
+  return y;
+}
+
+template <typename T> struct Mma;
+template <> struct Mma<_Float16> {
+  static __device__ __forceinline__ f4 qk(uint4 a, uint4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast_<h8>(a), bitcast_<h8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f4 pv(uint2 a, uint2 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast_<h4>(a), bitcast_<h4>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    _Float16 a = (_Float16)x, b = (_Float16)y;
+    return (uint32_t)bitcast_<uint16_t>(a) | ((uint32_t)bitcast_<uint16_t>(b) << 16);
+  }
+};
+template <> struct Mma<__hip_bfloat16> {
+  static __device__ __forceinline__ f4 qk(uint4 a, uint4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast_<bf8>(a), bitcast_<bf8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f4 pv(uint2 a, uint2 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bitcast_<s4>(a), bitcast_<s4>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    __hip_bfloat16 a = __float2bfloat16(x), b = __float2bfloat16(y);
+    return (uint32_t)bitcast_<uint16_t>(a) | ((uint32_t)bitcast_<uint16_t>(b) << 16);
+  }
+};
+
+// Chunk swizzle of the staged V tile: 16-byte chunk c of token row t lives at c ^ vswz(t).
+// Row writes (one row per 16 lanes) stay 16-byte aligned and conflict-free, and the
+// transposing operand read (rows 4g..4g+3, 32 bytes each, per 16-lane group g) lands the
+// four rows of a group, and the two groups of a 32-lane half, on disjoint banks.
+template <int D>
+__device__ __forceinline__ int vswz(int t) {
+  return D == 128 ? 2 * (t & 7) : 2 * ((t >> 1) & 3);
+}
+
+typedef short s4v __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element (i & 3) of the
+// 8-byte rows addressed by lanes 4j + (i >> 2), j = 0..3.  With lane i of group g pointing
+// at V[4g + i/4][16*mt + 4*(i%4)], lane i gets V[4g + j][16*mt + i]: the V^T operand of the
+// 16x16x16 P.V product, in one instruction.
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  s4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4v*)(p));
+  uint2 u;
+  __builtin_memcpy(&u, &r, sizeof(u));
+  return u;
+}
+
+}  // namespace mfma
+}  // namespace pkv

@@ -1,0 +1,374 @@
+// Paged chunked prefill on the matrix cores (fp16 / bf16 caches, page_size 16, head_dim 64 or
+// 128, GQA group g in {1, 2, 4, 8, 16}).  Same contract as the vector kernel
+// (BatchPrefillWithPagedKVCacheWrapper.run, ecahlang/main.py:432-443, :68): query row i of
+// request b (qo_len_b rows) attends keys j <= i + kv_len_b - qo_len_b when causal (bottom-right
+// aligned), else all kv_len_b keys.
+//
+// Work items come from the host plan (one int32 record each, longest first):
+//   item = (request, KV head, 256 / g query tokens, a chunk [k0, k1) of the keys they see)
+// A workgroup of 8 waves owns the item's 256 query rows (row r = token r / g, head r % g of the
+// KV head's group), so every staged K/V page serves g * 256 / g = 256 rows.  Per 32 keys (two
+// pages), staged in LDS by all threads and double-buffered:
+//   S^T[key][row] = K . Q^T      v_mfma_f32_16x16x32, A = K from LDS, B = Q in registers
+//   online softmax per row in the accumulator layout (lane = row l % 16, keys 4*(l/16) + i)
+//   O^T[dim][row] += V^T . P     v_mfma_f32_16x16x16, A = V^T by ds_read_b64_tr_b16, B = P
+// Each wave owns 32 rows outright, so waves never combine.  An item that is one chunk of a
+// longer key range writes a partial (normalised rows plus running max and sum); the merge
+// kernel folds the partials of each split group.
+#include "attn_common.h"
+#include "mfma_common.h"
+#include "../../include/pagedkv.h"
+
+using namespace pkv;
+using namespace pkv::mfma;
+
+namespace {
+
+constexpr int kRows = 256;   // query rows per item (8 waves x 32)
+constexpr int kItem = 12;    // int32 fields per work item
+constexpr int kGroup = 8;    // int32 fields per split group
+
+struct PrefillMfmaParams {
+  const void* q;
+  int64_t q_sn, q_sh;
+  const void* k_cache;
+  const void* v_cache;
+  int64_t page_stride, num_pages;
+  const int32_t* indices;
+  int64_t num_indices;
+  int32_t hq, hkv;
+  int32_t causal;
+  float scale_log2;
+  void* out;
+  int64_t o_sn, o_sh;
+  const int32_t* items;
+  float2* part_ml;  // [slot][kRows]
+  float* part_o;    // [slot][kRows][D]
+  int32_t o_vec;
+};
+
+// K staged row-major, 16-byte chunk c of key row t at c ^ kswz(t): the A-operand read (16 keys,
+// one chunk per 16-lane group) then touches distinct banks.
+template <int D>
+__device__ __forceinline__ int kswz(int t) {
+  return D == 128 ? (t & 15) : (t & 7);
+}
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) {
+  constexpr int KSTEPS = D / 32;      // Q.K^T reduction steps
+  constexpr int MT = D / 16;          // output tiles of 16 dims
+  constexpr int CPR = D / 8;          // 16-byte chunks per row
+  constexpr int ROWB = D * 2;         // bytes per staged row
+  constexpr int TILEB = 16 * ROWB;    // bytes per staged page (16 rows)
+  constexpr int STEPB = 2 * TILEB;    // two pages
+  constexpr int CHUNKS = 2 * 2 * 16 * CPR;  // K and V chunks of one step
+  constexpr int CPT = CHUNKS / 512;   // chunks per thread
+  static_assert(CHUNKS % 512 == 0, "chunks per thread");
+  constexpr int TQ = kRows / G;       // query tokens per item
+
+  __shared__ __align__(16) char s_k[2][STEPB];
+  __shared__ __align__(16) char s_v[2][STEPB];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+
+  const int32_t* it = P.items + (int64_t)kItem * blockIdx.x;
+  const int h = it[1], t0 = it[2], tq = it[3], k0 = it[4], k1 = it[5], slot = it[6];
+  const int kv_len = it[7], qo_len = it[8], qo_start = it[9], kp0 = it[10];
+  const int64_t npages_req = (kv_len + 15) / 16;
+
+  const T* kc = reinterpret_cast<const T*>(P.k_cache);
+  const T* vc = reinterpret_cast<const T*>(P.v_cache);
+  const int64_t rowstride = (int64_t)P.hkv * D;
+  const int64_t hoff = (int64_t)h * D;
+
+  // ---- this wave's 32 rows: Q^T operand in registers (B of the 16x16x32 product)
+  uint4 qr[2][KSTEPS];
+  int rtok[2];  // token (within the item) of this lane's row in each row tile
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = 32 * wave + 16 * rt + lr;
+    const int tt = r / G, hh = r % G;
+    rtok[rt] = tt;
+    const bool ok = tt < tq;
+    const T* src = reinterpret_cast<const T*>(P.q) + (int64_t)(qo_start + t0 + (ok ? tt : 0)) * P.q_sn +
+                   (int64_t)(h * G + hh) * P.q_sh + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      const uint4 v = *reinterpret_cast<const uint4*>(src + 32 * s);
+      qr[rt][s] = ok ? v : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // ---- staging: step st covers keys kb = k0 + 32 st .. +31 (pages kb/16, kb/16 + 1)
+  const int nsteps = (k1 - k0 + 31) / 32;
+  auto page_of = [&](int key) __attribute__((always_inline)) -> int64_t {  // -1: absent page
+    const int64_t pi = key / 16;
+    int64_t e = kp0 + (pi < npages_req ? pi : npages_req - 1);
+    e = e < P.num_indices ? e : P.num_indices - 1;
+    const int64_t pg = e >= 0 ? P.indices[e] : -1;
+    return (pg >= 0 && pg < P.num_pages) ? pg : -1;
+  };
+  uint4 stage[CPT];
+  auto load_step = [&](int st) __attribute__((always_inline)) {
+    const int kb = k0 + 32 * st;
+    const int64_t pg0 = page_of(kb), pg1 = page_of(kb + 16);
+#pragma unroll
+    for (int x = 0; x < CPT; ++x) {
+      const int c = threadIdx.x + 512 * x;
+      const int p = c / (2 * 16 * CPR), kv = (c / (16 * CPR)) & 1, row = (c / CPR) & 15, col = c % CPR;
+      const int64_t pg = p ? pg1 : pg0;
+      const T* base = kv ? vc : kc;
+      const T* src = base + (pg < 0 ? 0 : pg) * P.page_stride + row * rowstride + hoff + 8 * col;
+      stage[x] = *reinterpret_cast<const uint4*>(src);
+    }
+  };
+  auto store_step = [&](int st, int buf) __attribute__((always_inline)) {
+    const int kb = k0 + 32 * st;
+    const int64_t pg0 = page_of(kb), pg1 = page_of(kb + 16);
+#pragma unroll
+    for (int x = 0; x < CPT; ++x) {
+      const int c = threadIdx.x + 512 * x;
+      const int p = c / (2 * 16 * CPR), kv = (c / (16 * CPR)) & 1, row = (c / CPR) & 15, col = c % CPR;
+      const int key = kb + 16 * p + row;
+      const bool absent = (p ? pg1 : pg0) < 0;
+      if (kv) {  // values past the chunk or in an absent page are zeroed: 0 * NaN would poison P.V
+        const uint4 val = (key < k1 && !absent) ? stage[x] : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(&s_v[buf][p * TILEB + row * ROWB + ((col ^ vswz<D>(row)) << 4)]) = val;
+      } else {
+        *reinterpret_cast<uint4*>(&s_k[buf][p * TILEB + row * ROWB + ((col ^ kswz<D>(row)) << 4)]) = stage[x];
+      }
+    }
+  };
+
+  f4 o[2][MT];
+  float m[2], lsum[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) o[rt][mt] = f4{0.f, 0.f, 0.f, 0.f};
+    m[rt] = -INFINITY;
+    lsum[rt] = 0.f;
+  }
+  // key limit of each row: j < lim (causal: bottom-right aligned diagonal)
+  int lim[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int tabs = t0 + rtok[rt];
+    int l = P.causal ? tabs + kv_len - qo_len + 1 : kv_len;
+    l = l < k1 ? l : k1;
+    lim[rt] = rtok[rt] < tq ? l : -1;
+  }
+
+  if (nsteps > 0) {
+    load_step(0);
+    store_step(0, 0);
+  }
+  lds_barrier();
+  for (int st = 0; st < nsteps; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nsteps) load_step(st + 1);
+    const int kb = k0 + 32 * st;
+    const bool abs0 = page_of(kb) < 0, abs1 = page_of(kb + 16) < 0;
+    // S^T tiles: [key tile kt][row tile rt]
+    f4 sacc[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const char* krow = &s_k[buf][kt * TILEB + lr * ROWB];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const uint4 a = *reinterpret_cast<const uint4*>(krow + (((4 * s + lg) ^ kswz<D>(lr)) << 4));
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = Mma<T>::qk(a, qr[rt][s], sacc[kt][rt]);
+      }
+    }
+    // masked online softmax per row tile; P packed as the B operand of the P.V product
+    uint2 pb[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float sv[2][4];
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const bool absent = kt ? abs1 : abs0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 16 * kt + 4 * lg + i;
+          sv[kt][i] = (key < lim[rt] && !absent) ? sacc[kt][rt][i] * P.scale_log2 : -INFINITY;
+          cmax = fmaxf(cmax, sv[kt][i]);
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      const float mnew = fmaxf(m[rt], cmax);
+      const float muse = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(m[rt] - muse);
+      float psum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[i] = __builtin_amdgcn_exp2f(sv[kt][i] - muse);
+          psum += pr[i];
+        }
+        pb[kt][rt] = make_uint2(Mma<T>::pack(pr[0], pr[1]), Mma<T>::pack(pr[2], pr[3]));
+      }
+      lsum[rt] = lsum[rt] * alpha + psum;
+      if (__ballot(mnew != m[rt])) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[rt][mt] *= alpha;
+      }
+      m[rt] = mnew;
+    }
+    // O^T += V^T . P
+    const int tr_row = 4 * lg + (lr >> 2);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const char* tr_base = &s_v[buf][kt * TILEB + tr_row * ROWB + (lr & 1) * 8];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int chunk = (2 * mt + ((lr & 3) >> 1)) ^ vswz<D>(tr_row);
+        const uint2 vt = lds_read_tr16(tr_base + (chunk << 4));
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) o[rt][mt] = Mma<T>::pv(vt, pb[kt][rt], o[rt][mt]);
+      }
+    }
+    if (st + 1 < nsteps) store_step(st + 1, buf ^ 1);
+    lds_barrier();  // the next buffer is staged; this one is free for the step after
+  }
+
+  // ---- rows out: normalised output rows, or the partial of a split group
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float ltot = lsum[rt] + __shfl_xor(lsum[rt], 16, 64);
+    ltot += __shfl_xor(ltot, 32, 64);
+    const int r = 32 * wave + 16 * rt + lr;
+    const int tt = rtok[rt], hh = r % G;
+    if (tt >= tq) continue;
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    if (slot < 0) {
+      T* orow = reinterpret_cast<T*>(P.out) + (int64_t)(qo_start + t0 + tt) * P.o_sn + (int64_t)(h * G + hh) * P.o_sh + 4 * lg;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (P.o_vec) {
+          *reinterpret_cast<uint2*>(orow + 16 * mt) = make_uint2(Mma<T>::pack(o[rt][mt][0] * inv, o[rt][mt][1] * inv),
+                                                                 Mma<T>::pack(o[rt][mt][2] * inv, o[rt][mt][3] * inv));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) orow[16 * mt + i] = from_f32<T>(o[rt][mt][i] * inv);
+        }
+      }
+    } else {
+      const int64_t pr = (int64_t)slot * kRows + r;
+      float* prow = P.part_o + pr * D + 4 * lg;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        *reinterpret_cast<float4*>(prow + 16 * mt) = make_float4(o[rt][mt][0] * inv, o[rt][mt][1] * inv,
+                                                                 o[rt][mt][2] * inv, o[rt][mt][3] * inv);
+      if (lg == 0) P.part_ml[pr] = make_float2(m[rt], ltot);
+    }
+  }
+}
+
+// Folds the partials of each split group: group = {first_slot, nslots, qo_start, t0, tq, h}.
+// One workgroup per group; an item is 4 dims of one row.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P, const int32_t* groups) {
+  const int32_t* gr = groups + (int64_t)kGroup * blockIdx.x;
+  const int s0 = gr[0], ns = gr[1], qo_start = gr[2], t0 = gr[3], tq = gr[4], h = gr[5];
+  for (int idx = threadIdx.x; idx < kRows * (D / 4); idx += blockDim.x) {
+    const int r = idx / (D / 4), d = (idx % (D / 4)) * 4;
+    const int tt = r / G, hh = r % G;
+    if (tt >= tq) continue;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, P.part_ml[(int64_t)(s0 + s) * kRows + r].x);
+    float den = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < ns; ++s) {
+      const int64_t pr = (int64_t)(s0 + s) * kRows + r;
+      const float2 ml = P.part_ml[pr];
+      const float c = ml.y > 0.f ? exp2f(ml.x - M) * ml.y : 0.f;
+      if (c == 0.f) continue;
+      const float4 v = *reinterpret_cast<const float4*>(P.part_o + pr * D + d);
+      den += c;
+      acc.x += c * v.x;
+      acc.y += c * v.y;
+      acc.z += c * v.z;
+      acc.w += c * v.w;
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    T* orow = reinterpret_cast<T*>(P.out) + (int64_t)(qo_start + t0 + tt) * P.o_sn + (int64_t)(h * G + hh) * P.o_sh + d;
+    orow[0] = from_f32<T>(acc.x * inv);
+    orow[1] = from_f32<T>(acc.y * inv);
+    orow[2] = from_f32<T>(acc.z * inv);
+    orow[3] = from_f32<T>(acc.w * inv);
+  }
+}
+
+template <typename T, int D, int G>
+int launch(const PrefillMfmaParams& P, int n_items, const int32_t* groups, int n_groups, hipStream_t s) {
+  if (n_items > 0)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, G>), dim3(n_items), dim3(512), 0, s, P);
+  if (n_groups > 0)
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, G>), dim3(n_groups), dim3(256), 0, s, P, groups);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int D>
+int launch_g(const PrefillMfmaParams& P, int g, int n_items, const int32_t* groups, int n_groups, hipStream_t s) {
+  switch (g) {
+    case 1: return launch<T, D, 1>(P, n_items, groups, n_groups, s);
+    case 2: return launch<T, D, 2>(P, n_items, groups, n_groups, s);
+    case 4: return launch<T, D, 4>(P, n_items, groups, n_groups, s);
+    case 8: return launch<T, D, 8>(P, n_items, groups, n_groups, s);
+    case 16: return launch<T, D, 16>(P, n_items, groups, n_groups, s);
+  }
+  return kBadGroup;
+}
+
+}  // namespace
+
+extern "C" int pkv_prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
+                                          int32_t num_kv_heads, int32_t page_size) {
+  if (num_kv_heads <= 0 || num_qo_heads % num_kv_heads) return 0;
+  const int g = num_qo_heads / num_kv_heads;
+  return (dtype == kF16 || dtype == kBF16) && (head_dim == 64 || head_dim == 128) && page_size == 16 &&
+         (g == 1 || g == 2 || g == 4 || g == 8 || g == 16);
+}
+
+extern "C" int pkv_batch_prefill_mfma(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                      const void* k_cache, const void* v_cache, int64_t page_stride,
+                                      int64_t num_pages, const int32_t* kv_indices, int64_t num_indices,
+                                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t page_size, int32_t causal, float sm_scale,
+                                      const int32_t* items, int32_t n_items, const int32_t* groups,
+                                      int32_t n_groups, void* part_ml, void* part_o, void* out,
+                                      int64_t o_stride_n, int64_t o_stride_h, int32_t dtype, void* stream) {
+  if (!pkv_prefill_mfma_supported(dtype, head_dim, num_qo_heads, num_kv_heads, page_size)) return kBadArg;
+  if (n_items < 0 || n_groups < 0 || (n_items > 0 && !items) || (n_groups > 0 && (!groups || !part_ml || !part_o)))
+    return kBadArg;
+  const int es = 2;
+  if ((uintptr_t)q % 16 || (q_stride_n * es) % 16 || (q_stride_h * es) % 16) return kBadAlign;
+  PrefillMfmaParams P;
+  P.q = q; P.q_sn = q_stride_n; P.q_sh = q_stride_h;
+  P.k_cache = k_cache; P.v_cache = v_cache; P.page_stride = page_stride; P.num_pages = num_pages;
+  P.indices = kv_indices; P.num_indices = num_indices;
+  P.hq = num_qo_heads; P.hkv = num_kv_heads; P.causal = causal;
+  P.scale_log2 = sm_scale * 1.4426950408889634f;
+  P.out = out; P.o_sn = o_stride_n; P.o_sh = o_stride_h;
+  P.items = items;
+  P.part_ml = reinterpret_cast<float2*>(part_ml);
+  P.part_o = reinterpret_cast<float*>(part_o);
+  P.o_vec = ((uintptr_t)out % 8 == 0) && ((o_stride_n * es) % 8 == 0) && ((o_stride_h * es) % 8 == 0);
+  hipStream_t s = (hipStream_t)stream;
+  const int g = num_qo_heads / num_kv_heads;
+  if (dtype == kF16)
+    return head_dim == 64 ? launch_g<_Float16, 64>(P, g, n_items, groups, n_groups, s)
+                          : launch_g<_Float16, 128>(P, g, n_items, groups, n_groups, s);
+  return head_dim == 64 ? launch_g<__hip_bfloat16, 64>(P, g, n_items, groups, n_groups, s)
+                        : launch_g<__hip_bfloat16, 128>(P, g, n_items, groups, n_groups, s);
+}

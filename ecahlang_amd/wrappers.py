@@ -210,11 +210,77 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if self._kv_dtype != self._q_dtype:
             raise NotImplementedError("q and kv must share one dtype")
         self._sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(self._d)
+        self._mfma = bool(lib().pkv_prefill_mfma_supported(dtype_code(self._q_dtype), self._d, self._hq,
+                                                          self._hkv, self._ps))
+        if self._mfma:
+            self._schedule(qo_indptr.device)
         self._planned = True
+
+    # rows per matrix-core work item (8 waves x 32 rows): 256 / g query tokens of one KV head
+    _ROWS = 256
+
+    def _schedule(self, dev: torch.device) -> None:
+        """The matrix-core kernel's work list.  Like FlashInfer's plan, this reads the (small)
+        indptr arrays back to the host once per batch.  Items are (request, KV head, 256/g query
+        tokens, chunk of the keys those tokens see); a long key range is cut into chunks so
+        that there are about two items per compute unit, and the chunks' partials are merged
+        by a second kernel.  Items are issued longest first."""
+        qo = self._qo_indptr.cpu().tolist()
+        kp = self._indptr.cpu().tolist()
+        last = self._last.cpu().tolist()
+        g = self._hq // self._hkv
+        tq_max = self._ROWS // g
+        groups = []  # (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b)
+        for b in range(self._batch):
+            qo_len = qo[b + 1] - qo[b]
+            npg = kp[b + 1] - kp[b]
+            kv_len = (npg - 1) * self._ps + last[b] if npg > 0 else 0
+            for t0 in range(0, qo_len, tq_max):
+                tq = min(tq_max, qo_len - t0)
+                kv_end = min(kv_len, max(0, t0 + tq + kv_len - qo_len)) if self._causal else kv_len
+                for h in range(self._hkv):
+                    groups.append((h, t0, tq, kv_end, kv_len, qo_len, qo[b], kp[b], b))
+        self._nnz_q = qo[-1]
+        total = sum(gr[3] for gr in groups)
+        chunk = max(256, min(1 << 20, -(-total // (2 * _num_cus(dev)) // 32) * 32 or 256))
+        ws_bytes = self._workspace.numel() * self._workspace.element_size()
+        while True:
+            items, merges, nslots = [], [], 0
+            for (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b) in groups:
+                nch = max(1, -(-kv_end // chunk))
+                if nch == 1:
+                    items.append([b, h, t0, tq, 0, kv_end, -1, kv_len, qo_len, qo_start, kp0, 0])
+                    continue
+                for c in range(nch):
+                    items.append([b, h, t0, tq, c * chunk, min(kv_end, (c + 1) * chunk), nslots + c, kv_len,
+                                  qo_len, qo_start, kp0, 0])
+                merges.append([nslots, nch, qo_start, t0, tq, h, 0, 0])
+                nslots += nch
+            a = lambda n: -(-n // 256) * 256
+            off_g = a(len(items) * 12 * 4)
+            off_ml = off_g + a(len(merges) * 8 * 4)
+            off_o = off_ml + a(nslots * self._ROWS * 8)
+            need = off_o + nslots * self._ROWS * self._d * 4
+            if need <= ws_bytes or not merges:
+                break
+            chunk *= 2
+        if need > ws_bytes:
+            raise RuntimeError(f"prefill workspace too small: need {need} bytes")
+        items.sort(key=lambda it: it[4] - it[5])  # longest key range first
+        flat = [x for it in items for x in it] + [0] * ((off_g - len(items) * 48) // 4) + \
+               [x for m in merges for x in m]
+        if flat:
+            host = torch.tensor(flat, dtype=torch.int32).pin_memory()
+            self._workspace.view(torch.uint8)[: 4 * len(flat)].view(torch.int32).copy_(host, non_blocking=True)
+        base = self._workspace.data_ptr()
+        self._n_items, self._n_groups = len(items), len(merges)
+        self._items_ptr, self._groups_ptr = base, base + off_g
+        self._ml_ptr, self._o_ptr = base + off_ml, base + off_o
+        self._chunk = chunk
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,
             v_scale=None, out: torch.Tensor | None = None, lse=None, return_lse: bool = False,
-            enable_pdl=None, window_left=None) -> torch.Tensor:
+            enable_pdl=None, window_left=None, force_valu: bool = False) -> torch.Tensor:
         if not self._planned:
             raise RuntimeError("plan() must be called before run()")
         if return_lse or lse is not None:
@@ -229,6 +295,20 @@ class BatchPrefillWithPagedKVCacheWrapper:
         nnz = q.shape[0]
         if out is None:
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+            raise ValueError("out must match q's shape and dtype")
+        aligned = q.data_ptr() % 16 == 0 and (q.stride(0) * q.element_size()) % 16 == 0 and \
+            (q.stride(1) * q.element_size()) % 16 == 0
+        if self._mfma and aligned and not force_valu:
+            if nnz < self._nnz_q:
+                raise ValueError(f"q has {nnz} rows, qo_indptr needs {self._nnz_q}")
+            check(lib().pkv_batch_prefill_mfma(
+                q.data_ptr(), q.stride(0), q.stride(1), cv.k_ptr, cv.v_ptr, cv.page_stride, cv.num_pages,
+                self._indices.data_ptr(), self._indices.numel(), self._hq, self._hkv, self._d, self._ps,
+                int(self._causal), self._sm_scale, self._items_ptr, self._n_items, self._groups_ptr,
+                self._n_groups, self._ml_ptr, self._o_ptr, out.data_ptr(), out.stride(0), out.stride(1),
+                dtype_code(q.dtype), stream_ptr(q.device)), "BatchPrefillWithPagedKVCacheWrapper.run")
+            return out
         check(lib().pkv_batch_prefill_valu(
             q.data_ptr(), q.stride(0), q.stride(1), self._qo_indptr.data_ptr(), nnz, cv.k_ptr,
             cv.v_ptr, cv.page_stride, cv.num_pages, self._indptr.data_ptr(),

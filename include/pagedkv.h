@@ -122,6 +122,27 @@ int pkv_batch_prefill_valu(const void* q, int64_t q_stride_n, int64_t q_stride_h
                            void* out, int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
                            void* stream);
 
+/* BatchPrefillWithPagedKVCacheWrapper.run on the matrix cores (same contract as
+ * pkv_batch_prefill_valu; ecahlang/main.py:432-443, :68) for fp16/bf16, head_dim 64 or 128,
+ * page_size 16 and GQA groups 1, 2, 4, 8, 16 (pkv_prefill_mfma_supported).  The work list comes
+ * from the wrapper's plan: n_items records of 12 int32 {request, kv_head, first query token,
+ * query tokens, key chunk begin, key chunk end, partial slot or -1, kv_len, qo_len, first q row,
+ * first page-list entry, 0}, each covering 256 / g query tokens; n_groups records of 8 int32
+ * {first slot, slots, first q row, first query token, query tokens, kv_head, 0, 0} name the
+ * split items whose partials (part_ml: float2 x 256 per slot, part_o: fp32 x 256 x head_dim per
+ * slot) a second kernel merges.  q must be 16-byte aligned with strides that keep rows
+ * aligned (PKV_E_ALIGN otherwise). */
+int pkv_prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
+                               int32_t num_kv_heads, int32_t page_size);
+int pkv_batch_prefill_mfma(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                           const void* k_cache, const void* v_cache, int64_t page_stride,
+                           int64_t num_pages, const int32_t* kv_indices, int64_t num_indices,
+                           int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t page_size, int32_t causal, float sm_scale,
+                           const int32_t* items, int32_t n_items, const int32_t* groups,
+                           int32_t n_groups, void* part_ml, void* part_o, void* out,
+                           int64_t o_stride_n, int64_t o_stride_h, int32_t dtype, void* stream);
+
 /* Page pool of AutoKVCacheManager (ecahlang/manager.py:56, 99-120, 187-212), device side.
  * stack[0 .. n_free) holds the free page ids (the reference's free_blocks list: pop() takes
  * the last entry, extend() appends in page order); table is rows x stride int32, one row of

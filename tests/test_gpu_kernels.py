@@ -345,6 +345,9 @@ PREFILL_CASES = {
     "bf16_ragged": lambda: workloads.build_batch([40, 200, 1, 64], [40, 17, 1, 3], 32, 8, 128,
                                                  torch.bfloat16, 51),
     "fp32_d64": lambda: workloads.build_batch([30, 90], [12, 30], 32, 8, 64, torch.float32, 52),
+    # matrix-core shapes: MHA at head_dim 64, a 16-head group, a query tile cut short
+    "mha_fp16_d64": lambda: workloads.build_batch([300, 70, 513], [300, 5, 100], 8, 8, 64, torch.float16, 53),
+    "g16_bf16_d64": lambda: workloads.build_batch([33, 600], [33, 40], 16, 1, 64, torch.bfloat16, 54),
 }
 
 
@@ -355,7 +358,7 @@ def test_prefill_matches_oracle(name, causal):
     print(f"case {name} causal={causal}: nnz={wb.q.shape[0]}", flush=True)
     dv = wb.to(DEV)
     _append_dev(dv)
-    ws = torch.empty(16 << 20, dtype=torch.uint8, device=DEV)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
     w = BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
     w.plan(dv.append_indptr, dv.indptr, dv.indices, dv.last, dv.hq, dv.hkv, dv.d, dv.ps,
            causal=causal, q_data_type=dv.dtype)
@@ -365,3 +368,27 @@ def test_prefill_matches_oracle(name, causal):
     ref = kv_ref.prefill(wb.q.float().numpy(), wb.append_indptr.numpy(), vals, wb.indptr.numpy(),
                          wb.indices.numpy(), wb.last.numpy(), wb.ps, causal=causal)
     np.testing.assert_allclose(o.float().cpu().numpy(), ref, **TOL[wb.dtype])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_chunked_qwen_full_size(causal):
+    # C3 at full size: 8 requests x 512-token chunks onto prefixes U[0, 8192]; the key ranges are
+    # cut into chunks whose partials the merge kernel folds, and the matrix-core result also
+    # agrees with the vector-ALU kernel
+    wb = workloads.qwen25_3b_prefill()
+    print(f"C3 causal={causal}: nnz={wb.q.shape[0]} kv={sum(wb.kv_len)}", flush=True)
+    dv = wb.to(DEV)
+    _append_dev(dv)
+    ws = torch.empty(128 << 20, dtype=torch.uint8, device=DEV)
+    w = BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w.plan(dv.append_indptr, dv.indptr, dv.indices, dv.last, dv.hq, dv.hkv, dv.d, dv.ps,
+           causal=causal, q_data_type=dv.dtype)
+    assert w._mfma and w._n_groups > 0  # split groups exercised
+    o = w.run(dv.q, dv.cache)
+    ov = w.run(dv.q, dv.cache, force_valu=True)
+    torch.cuda.synchronize()
+    _, vals = _oracle_appended(wb)
+    ref = kv_ref.prefill(wb.q.float().numpy(), wb.append_indptr.numpy(), vals, wb.indptr.numpy(),
+                         wb.indices.numpy(), wb.last.numpy(), wb.ps, causal=causal)
+    np.testing.assert_allclose(o.float().cpu().numpy(), ref, **TOL[wb.dtype])
+    np.testing.assert_allclose(ov.float().cpu().numpy(), ref, **TOL[wb.dtype])
