@@ -7,12 +7,17 @@
 // Work items come from the host plan (one int32 record each, longest first):
 //   item = (request, KV head, 256 / g query tokens, a chunk [k0, k1) of the keys they see)
 // A workgroup of 8 waves owns the item's 256 query rows (row r = token r / g, head r % g of the
-// KV head's group), so every staged K/V page serves g * 256 / g = 256 rows.  Per 32 keys (two
-// pages), staged in LDS by all threads and double-buffered:
+// KV head's group), so every staged K/V page serves all 256 rows.  Per 64 keys (four pages),
+// staged in LDS by all threads and double-buffered:
 //   S^T[key][row] = K . Q^T      v_mfma_f32_16x16x32, A = K from LDS, B = Q in registers
 //   online softmax per row in the accumulator layout (lane = row l % 16, keys 4*(l/16) + i)
-//   O^T[dim][row] += V^T . P     v_mfma_f32_16x16x16, A = V^T by ds_read_b64_tr_b16, B = P
-// Each wave owns 32 rows outright, so waves never combine.  An item that is one chunk of a
+//   O^T[dim][row] += V^T . P     v_mfma_f32_16x16x32 over two pages at a time: the reduction
+//                                slot 8*(l/16) + e holds key 4*(l/16) + e of the first page for
+//                                e < 4 and of the second for e >= 4, which is where the softmax
+//                                left P and where two ds_read_b64_tr_b16 leave V^T
+// Pages go global -> LDS directly (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l),
+// three steps in flight, so no registers hold them on the way.  Each wave owns 32 rows
+// outright, so waves never combine.  An item that is one chunk of a
 // longer key range writes a partial (normalised rows plus running max and sum); the merge
 // kernel folds the partials of each split group.
 #include "attn_common.h"
@@ -25,6 +30,27 @@ using namespace pkv::mfma;
 namespace {
 
 constexpr int kRows = 256;   // query rows per item (8 waves x 32)
+constexpr int kStepPages = 4;  // pages (16 keys each) staged per step; chunks start at multiples of 64 keys
+constexpr int kMaxChunk = 8192;  // keys per item (its page ids are staged in LDS)
+
+// Source of the value rows that must read as zero (past the chunk, absent pages): P is 0 there,
+// and 0 * NaN would poison P.V.
+__device__ uint4 g_zero_rows[64];
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// One wave-wide 16-byte-per-lane copy global -> LDS: lane l's 16 bytes at src (per lane) land at
+// LDS byte dst + 16 * l (dst uniform across the wave, passed in M0).  Written as inline assembly
+// so that the compiler does not track it: the caller orders it with explicit vmcnt waits and
+// barriers (the compiler cannot tell which LDS array a later transposed read touches and would
+// otherwise wait for every copy in flight, draining the prefetch pipeline).
+__device__ __forceinline__ void lds_copy16(const void* src, const char* dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
 constexpr int kItem = 12;    // int32 fields per work item
 constexpr int kGroup = 8;    // int32 fields per split group
 
@@ -61,14 +87,19 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
   constexpr int CPR = D / 8;          // 16-byte chunks per row
   constexpr int ROWB = D * 2;         // bytes per staged row
   constexpr int TILEB = 16 * ROWB;    // bytes per staged page (16 rows)
-  constexpr int STEPB = 2 * TILEB;    // two pages
-  constexpr int CHUNKS = 2 * 2 * 16 * CPR;  // K and V chunks of one step
-  constexpr int CPT = CHUNKS / 512;   // chunks per thread
-  static_assert(CHUNKS % 512 == 0, "chunks per thread");
+  constexpr int NP = kStepPages;
+  constexpr int STEPB = NP * TILEB;   // one step's pages
+  constexpr int RPI = 64 / CPR;       // rows per 1 KB direct load (one 16-byte chunk per lane)
+  constexpr int LPP = 16 / RPI;       // loads per page and K or V
+  constexpr int LPW = NP * 2 * LPP / 8;  // loads per wave per step
+  static_assert(NP * 2 * LPP % 8 == 0, "loads per wave");
   constexpr int TQ = kRows / G;       // query tokens per item
 
-  __shared__ __align__(16) char s_k[2][STEPB];
-  __shared__ __align__(16) char s_v[2][STEPB];
+  // three stages as distinct arrays (the step loop is unrolled by three): the compiler can then
+  // tell the stage being read from the stages being filled and does not wait for the latter
+  __shared__ __align__(16) char s_k0[STEPB], s_k1[STEPB], s_k2[STEPB];
+  __shared__ __align__(16) char s_v0[STEPB], s_v1[STEPB], s_v2[STEPB];
+  __shared__ int s_page[kMaxChunk / 16 + kStepPages];  // the chunk's page ids, -1 = absent
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
@@ -101,44 +132,52 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     }
   }
 
-  // ---- staging: step st covers keys kb = k0 + 32 st .. +31 (pages kb/16, kb/16 + 1)
-  const int nsteps = (k1 - k0 + 31) / 32;
-  auto page_of = [&](int key) __attribute__((always_inline)) -> int64_t {  // -1: absent page
-    const int64_t pi = key / 16;
+  // ---- staging: step st covers keys kb = k0 + 64 st .. +63 (pages kb/16 .. kb/16 + 3)
+  // (the plan keeps k1 - k0 <= kMaxChunk; the clamp keeps s_page in bounds regardless)
+  const int nsteps = min((k1 - k0 + 16 * NP - 1) / (16 * NP), kMaxChunk / (16 * NP));
+  // the chunk's page ids (pages past the request's last one repeat it; their keys are masked)
+  const int npc = nsteps * NP;
+  for (int i = threadIdx.x; i < npc; i += blockDim.x) {
+    const int64_t pi = k0 / 16 + i;
     int64_t e = kp0 + (pi < npages_req ? pi : npages_req - 1);
     e = e < P.num_indices ? e : P.num_indices - 1;
     const int64_t pg = e >= 0 ? P.indices[e] : -1;
-    return (pg >= 0 && pg < P.num_pages) ? pg : -1;
+    s_page[i] = (pg >= 0 && pg < P.num_pages) ? (int)pg : -1;
+  }
+  // the Q loads are complete here; a compiler-visible vmcnt(0) (expcnt, lgkmcnt at their maxima)
+  // tells the compiler so, which keeps it from waiting on them, and on every copy in flight,
+  // inside the step loop
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  lds_barrier();
+  auto page_of = [&](int key) __attribute__((always_inline)) -> int {  // -1: absent page
+    return s_page[(key - k0) / 16];
   };
-  uint4 stage[CPT];
-  auto load_step = [&](int st) __attribute__((always_inline)) {
-    const int kb = k0 + 32 * st;
-    const int64_t pg0 = page_of(kb), pg1 = page_of(kb + 16);
+  // Step st's pages into stage buf: wave-load wi (this wave: wi = wave * LPW + x) covers RPI
+  // rows of one page's K or V; lane l fills LDS slot l, i.e. row RPI*(wi % LPP) + l / CPR,
+  // position l % CPR, which holds the row's chunk position ^ swizzle(row).
+  auto issue_step = [&](int st, char* kstage, char* vstage) __attribute__((always_inline)) {
+    const int kb = k0 + 16 * NP * st;
 #pragma unroll
-    for (int x = 0; x < CPT; ++x) {
-      const int c = threadIdx.x + 512 * x;
-      const int p = c / (2 * 16 * CPR), kv = (c / (16 * CPR)) & 1, row = (c / CPR) & 15, col = c % CPR;
-      const int64_t pg = p ? pg1 : pg0;
-      const T* base = kv ? vc : kc;
-      const T* src = base + (pg < 0 ? 0 : pg) * P.page_stride + row * rowstride + hoff + 8 * col;
-      stage[x] = *reinterpret_cast<const uint4*>(src);
-    }
-  };
-  auto store_step = [&](int st, int buf) __attribute__((always_inline)) {
-    const int kb = k0 + 32 * st;
-    const int64_t pg0 = page_of(kb), pg1 = page_of(kb + 16);
-#pragma unroll
-    for (int x = 0; x < CPT; ++x) {
-      const int c = threadIdx.x + 512 * x;
-      const int p = c / (2 * 16 * CPR), kv = (c / (16 * CPR)) & 1, row = (c / CPR) & 15, col = c % CPR;
+    for (int x = 0; x < LPW; ++x) {
+      const int wi = wave * LPW + x;
+      const int p = wi / (2 * LPP), kv = (wi / LPP) & 1, r0 = RPI * (wi % LPP);
+      const int row = r0 + lane / CPR, pos = lane % CPR;
+      const int pg = page_of(kb + 16 * p);
       const int key = kb + 16 * p + row;
-      const bool absent = (p ? pg1 : pg0) < 0;
-      if (kv) {  // values past the chunk or in an absent page are zeroed: 0 * NaN would poison P.V
-        const uint4 val = (key < k1 && !absent) ? stage[x] : make_uint4(0, 0, 0, 0);
-        *reinterpret_cast<uint4*>(&s_v[buf][p * TILEB + row * ROWB + ((col ^ vswz<D>(row)) << 4)]) = val;
+      const void* src;
+      char* dst;
+      if (kv) {
+        const int col = pos ^ vswz<D>(row);
+        src = (pg < 0 || key >= k1) ? (const void*)(g_zero_rows + lane)
+                                    : (const void*)(vc + (int64_t)pg * P.page_stride + row * rowstride + hoff + 8 * col);
+        dst = vstage + p * TILEB + r0 * ROWB;
       } else {
-        *reinterpret_cast<uint4*>(&s_k[buf][p * TILEB + row * ROWB + ((col ^ kswz<D>(row)) << 4)]) = stage[x];
+        const int col = pos ^ kswz<D>(row);
+        src = (pg < 0) ? (const void*)(g_zero_rows + lane)
+                       : (const void*)(kc + (int64_t)pg * P.page_stride + row * rowstride + hoff + 8 * col);
+        dst = kstage + p * TILEB + r0 * ROWB;
       }
+      lds_copy16(src, dst);
     }
   };
 
@@ -161,21 +200,24 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     lim[rt] = rtok[rt] < tq ? l : -1;
   }
 
-  if (nsteps > 0) {
-    load_step(0);
-    store_step(0, 0);
-  }
-  lds_barrier();
-  for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nsteps) load_step(st + 1);
-    const int kb = k0 + 32 * st;
-    const bool abs0 = page_of(kb) < 0, abs1 = page_of(kb + 16) < 0;
-    // S^T tiles: [key tile kt][row tile rt]
-    f4 sacc[2][2];
+  // step st: compute on stage (ks, vs) = stage st % 3, refill stage (kn, vn) with step st + 2
+  auto do_step = [&](int st, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
+    // this wave's loads of step st are done (step st + 1's may still be in flight) ...
+    if (st + 1 < nsteps) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
+    // ... and every wave's: step st is staged, and every wave is past step st - 1, whose
+    // stage is refilled next
+    lds_barrier();
+    if (st + 2 < nsteps) issue_step(st + 2, kn, vn);
+    const int kb = k0 + 16 * NP * st;
+    bool absent[NP];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const char* krow = &s_k[buf][kt * TILEB + lr * ROWB];
+    for (int kt = 0; kt < NP; ++kt) absent[kt] = page_of(kb + 16 * kt) < 0;
+    // S^T tiles: [key tile kt][row tile rt]
+    f4 sacc[NP][2];
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) {
+      const char* krow = ks + kt * TILEB + lr * ROWB;
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -186,18 +228,17 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
       }
     }
     // masked online softmax per row tile; P packed as the B operand of the P.V product
-    uint2 pb[2][2];
+    uint2 pb[NP][2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float sv[2][4];
+      float sv[NP][4];
       float cmax = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const bool absent = kt ? abs1 : abs0;
+      for (int kt = 0; kt < NP; ++kt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kb + 16 * kt + 4 * lg + i;
-          sv[kt][i] = (key < lim[rt] && !absent) ? sacc[kt][rt][i] * P.scale_log2 : -INFINITY;
+          sv[kt][i] = (key < lim[rt] && !absent[kt]) ? sacc[kt][rt][i] * P.scale_log2 : -INFINITY;
           cmax = fmaxf(cmax, sv[kt][i]);
         }
       }
@@ -208,7 +249,7 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
       const float alpha = __builtin_amdgcn_exp2f(m[rt] - muse);
       float psum = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+      for (int kt = 0; kt < NP; ++kt) {
         float pr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -224,21 +265,32 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
       }
       m[rt] = mnew;
     }
-    // O^T += V^T . P
+    // O^T += V^T . P, two pages per 16x16x32 product
     const int tr_row = 4 * lg + (lr >> 2);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const char* tr_base = &s_v[buf][kt * TILEB + tr_row * ROWB + (lr & 1) * 8];
+    for (int u = 0; u < NP / 2; ++u) {
+      const char* tra = vs + (2 * u) * TILEB + tr_row * ROWB + (lr & 1) * 8;
+      const char* trb = tra + TILEB;
+      uint4 pp[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        pp[rt] = make_uint4(pb[2 * u][rt].x, pb[2 * u][rt].y, pb[2 * u + 1][rt].x, pb[2 * u + 1][rt].y);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int chunk = (2 * mt + ((lr & 3) >> 1)) ^ vswz<D>(tr_row);
-        const uint2 vt = lds_read_tr16(tr_base + (chunk << 4));
+        const int chunk = ((2 * mt + ((lr & 3) >> 1)) ^ vswz<D>(tr_row)) << 4;
+        const uint2 va = lds_read_tr16(tra + chunk), vb = lds_read_tr16(trb + chunk);
+        const uint4 vt = make_uint4(va.x, va.y, vb.x, vb.y);
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) o[rt][mt] = Mma<T>::pv(vt, pb[kt][rt], o[rt][mt]);
+        for (int rt = 0; rt < 2; ++rt) o[rt][mt] = Mma<T>::qk(vt, pp[rt], o[rt][mt]);
       }
     }
-    if (st + 1 < nsteps) store_step(st + 1, buf ^ 1);
-    lds_barrier();  // the next buffer is staged; this one is free for the step after
+  };
+  if (nsteps > 0) issue_step(0, s_k0, s_v0);
+  if (nsteps > 1) issue_step(1, s_k1, s_v1);
+  for (int st = 0; st < nsteps; st += 3) {
+    do_step(st, s_k0, s_v0, s_k2, s_v2);
+    if (st + 1 < nsteps) do_step(st + 1, s_k1, s_v1, s_k0, s_v0);
+    if (st + 2 < nsteps) do_step(st + 2, s_k2, s_v2, s_k1, s_v1);
   }
 
   // ---- rows out: normalised output rows, or the partial of a split group

@@ -242,7 +242,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                     groups.append((h, t0, tq, kv_end, kv_len, qo_len, qo[b], kp[b], b))
         self._nnz_q = qo[-1]
         total = sum(gr[3] for gr in groups)
-        chunk = max(256, min(1 << 20, -(-total // (2 * _num_cus(dev)) // 32) * 32 or 256))
+        # chunks are whole steps of the kernel (64 keys)
+        chunk = max(256, min(8192, -(-total // (2 * _num_cus(dev)) // 64) * 64 or 256))
         ws_bytes = self._workspace.numel() * self._workspace.element_size()
         while True:
             items, merges, nslots = [], [], 0
@@ -261,9 +262,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
             off_ml = off_g + a(len(merges) * 8 * 4)
             off_o = off_ml + a(nslots * self._ROWS * 8)
             need = off_o + nslots * self._ROWS * self._d * 4
-            if need <= ws_bytes or not merges:
+            if need <= ws_bytes or not merges or chunk >= 8192:
                 break
-            chunk *= 2
+            chunk = min(8192, chunk * 2)
         if need > ws_bytes:
             raise RuntimeError(f"prefill workspace too small: need {need} bytes")
         items.sort(key=lambda it: it[4] - it[5])  # longest key range first
