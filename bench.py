@@ -161,6 +161,12 @@ def chunked_prefill(args, torch, workloads, ops, dev):
     w.plan(dv.append_indptr, dv.indptr, dv.indices, dv.last, wb.hq, wb.hkv, wb.d, wb.ps, causal=True,
            q_data_type=wb.dtype)
     out = torch.empty_like(dv.q)
+    if args.profile_launches:
+        for _ in range(args.profile_launches):
+            w.run(dv.q, dv.cache, out=out)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_launches": args.profile_launches, "work_items": w._n_items}), flush=True)
+        return
     stream = torch.cuda.Stream(device=dev)
 
     def timed_graph(fn, reps, n):

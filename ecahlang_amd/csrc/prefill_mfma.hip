@@ -327,33 +327,63 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
 }
 
 // Folds the partials of each split group: group = {first_slot, nslots, qo_start, t0, tq, h}.
-// One workgroup per group; an item is 4 dims of one row.
+// A workgroup takes kMergeRows rows of one group; D/4 lanes per row, 4 dims each.  Loads are
+// issued kMergeUnroll slots at a time from clamped (always valid) addresses, so that they are
+// in flight together.
+constexpr int kMergeUnroll = 4;
+template <int D>
+constexpr int merge_rows() { return 256 / (D / 4); }
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P, const int32_t* groups) {
-  const int32_t* gr = groups + (int64_t)kGroup * blockIdx.x;
+  constexpr int RB = merge_rows<D>(), TPR = D / 4;
+  const int32_t* gr = groups + (int64_t)kGroup * (blockIdx.x / (kRows / RB));
   const int s0 = gr[0], ns = gr[1], qo_start = gr[2], t0 = gr[3], tq = gr[4], h = gr[5];
-  for (int idx = threadIdx.x; idx < kRows * (D / 4); idx += blockDim.x) {
-    const int r = idx / (D / 4), d = (idx % (D / 4)) * 4;
-    const int tt = r / G, hh = r % G;
-    if (tt >= tq) continue;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, P.part_ml[(int64_t)(s0 + s) * kRows + r].x);
-    float den = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < ns; ++s) {
-      const int64_t pr = (int64_t)(s0 + s) * kRows + r;
-      const float2 ml = P.part_ml[pr];
-      const float c = ml.y > 0.f ? exp2f(ml.x - M) * ml.y : 0.f;
-      if (c == 0.f) continue;
-      const float4 v = *reinterpret_cast<const float4*>(P.part_o + pr * D + d);
-      den += c;
-      acc.x += c * v.x;
-      acc.y += c * v.y;
-      acc.z += c * v.z;
-      acc.w += c * v.w;
+  const int r = (blockIdx.x % (kRows / RB)) * RB + threadIdx.x / TPR, d = (threadIdx.x % TPR) * 4;
+  const int tt = r / G, hh = r % G;
+  if (tt >= tq || ns <= 0) return;
+  const float2* ml = P.part_ml + (int64_t)s0 * kRows + r;
+  const float* po = P.part_o + ((int64_t)s0 * kRows + r) * D + d;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; s += kMergeUnroll) {
+    float2 v[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) v[u] = ml[(int64_t)min(s + u, ns - 1) * kRows];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) M = fmaxf(M, v[u].x);
+  }
+  float den = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s = 0; s < ns; s += kMergeUnroll) {
+    float2 w[kMergeUnroll];
+    float4 v[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int64_t sl = min(s + u, ns - 1);
+      w[u] = ml[sl * kRows];
+      v[u] = *reinterpret_cast<const float4*>(po + sl * kRows * D);
     }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    T* orow = reinterpret_cast<T*>(P.out) + (int64_t)(qo_start + t0 + tt) * P.o_sn + (int64_t)(h * G + hh) * P.o_sh + d;
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      // a slot whose rows saw no key (l = 0) carries no weight; repeats past ns count zero
+      // (such a slot's row may hold anything, hence the branch rather than a zero weight)
+      const float c = (s + u < ns && w[u].y > 0.f) ? exp2f(w[u].x - M) * w[u].y : 0.f;
+      if (c != 0.f) {
+        den += c;
+        acc.x += c * v[u].x;
+        acc.y += c * v[u].y;
+        acc.z += c * v[u].z;
+        acc.w += c * v[u].w;
+      }
+    }
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  T* orow = reinterpret_cast<T*>(P.out) + (int64_t)(qo_start + t0 + tt) * P.o_sn + (int64_t)(h * G + hh) * P.o_sh + d;
+  if (P.o_vec) {
+    T v[4] = {from_f32<T>(acc.x * inv), from_f32<T>(acc.y * inv), from_f32<T>(acc.z * inv),
+              from_f32<T>(acc.w * inv)};
+    *reinterpret_cast<uint2*>(orow) = *reinterpret_cast<const uint2*>(v);
+  } else {
     orow[0] = from_f32<T>(acc.x * inv);
     orow[1] = from_f32<T>(acc.y * inv);
     orow[2] = from_f32<T>(acc.z * inv);
@@ -366,7 +396,8 @@ int launch(const PrefillMfmaParams& P, int n_items, const int32_t* groups, int n
   if (n_items > 0)
     hipLaunchKernelGGL((prefill_mfma_kernel<T, D, G>), dim3(n_items), dim3(512), 0, s, P);
   if (n_groups > 0)
-    hipLaunchKernelGGL((prefill_merge_kernel<T, D, G>), dim3(n_groups), dim3(256), 0, s, P, groups);
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, G>), dim3(n_groups * (kRows / merge_rows<D>())), dim3(256), 0, s,
+                       P, groups);
   return (int)hipGetLastError();
 }
 
