@@ -146,6 +146,132 @@ def long_context(args, torch, workloads, Wrapper, dev):
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 
 
+def step36(args, torch, workloads, dev):
+    """The 36-layer decode step at Qwen2.5-3B attention shape, batch 128, on a shared
+    2048-token prefix (workloads.SharedPrefixDecodeLoop): per step, the host bookkeeping and
+    device page-table build (append_tokens, fill_cuda_graph_metadata, plan) plus one graph
+    replay of 36 x (append + decode).  The timed region of each step runs from before the
+    bookkeeping to the end of the replay; retiring 8 sequences and writing their successors'
+    tokens (the work of a prefill) happens between timed regions."""
+    import numpy as np
+    steps, warmup = max(1, min(args.steps, 40)), max(1, min(args.warmup, 4))
+    print("bench: building the 36-layer shared-prefix decode loop (B=128)", file=sys.stderr, flush=True)
+    loop = workloads.SharedPrefixDecodeLoop(dev, max_steps=steps + warmup + 2)
+    for _ in range(warmup):
+        loop.begin_step()
+        loop.replay()
+        loop.retire()
+    torch.cuda.synchronize()
+    times, byts = [], []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(loop.stream)
+        loop.begin_step()
+        loop.replay()
+        e1.record(loop.stream)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3)
+        byts.append(loop.step_bytes())
+        loop.retire()
+    # parity on the last step's layers 0 and 35, 8 sequences each, before the next step
+    par = None
+    if not args.no_check:
+        loop.begin_step()
+        loop.replay()
+        torch.cuda.synchronize()
+        par = step36_parity(loop, [0, loop.layers - 1], 8)
+    # the graph alone, replayed back to back (each replay repeats the same appends)
+    REP = 10
+    with torch.cuda.stream(loop.stream):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(loop.stream)
+        for _ in range(REP):
+            loop.graph.replay()
+        e1.record(loop.stream)
+    e1.synchronize()
+    t_graph = e0.elapsed_time(e1) / 1e3 / REP
+    L = loop.layers
+    t_step = float(np.mean(times))
+    uniq = float(np.mean([b["unique"] for b in byts])) * L
+    logical = float(np.mean([b["logical"] for b in byts])) * L
+    gbs = uniq / t_step / 1e9
+    gbs_graph = loop.step_bytes()["unique"] * L / t_graph / 1e9
+    # CPU baseline: the reference's path (gather + fp32 SDPA per sequence, index_put append)
+    # for one layer of 4 sequences
+    import torch.nn.functional as F
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cache0 = loop.mgr.kv_cache[0]
+    m = loop.mgr
+    sample = loop.ids[:4]
+    ks, vs, qs = [], [], []
+    for r, sid in enumerate(sample):
+        n = m._npages[sid]
+        pages = m._table[m.batch_to_seq_len[sid], :n].long()
+        Ls = m._seq_len(sid)
+        ks.append(cache0[pages, 0].reshape(-1, loop.hkv, loop.d)[:Ls].cpu())
+        vs.append(cache0[pages, 1].reshape(-1, loop.hkv, loop.d)[:Ls].cpu())
+        qs.append(loop.q[0, r].cpu())
+    ctimes = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for k, v, q in zip(ks, vs, qs):
+            F.scaled_dot_product_attention(q.float()[None, :, None, :], k.float().transpose(0, 1)[None],
+                                           v.float().transpose(0, 1)[None], enable_gqa=True)
+        ctimes.append(time.perf_counter() - t0)
+    sample_bytes = sum(k.numel() * 2 * 2 for k in ks)
+    result = {
+        "metric": "36-layer decode step (attention path), unique KV GB/s (% HBM peak), Qwen2.5-3B B=128 shared prefix",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "fp16", "data": "synthetic (device-generated N(0,1)*0.5, pages from the manager's pool, NaN-poisoned)",
+        "config": {"workload": "qwen2.5-3b 36-layer decode step, B=128, 2048-token shared prefix + own suffix U[64,1024], "
+                               "graph-captured append + decode per layer, 8 sequences retired per step",
+                   "layers": L, "batch": loop.batch, "steps": steps, "warmup": warmup,
+                   "pool_pages": loop.mgr.max_blocks},
+        "step_ms": round(t_step * 1e3, 4), "graph_ms": round(t_graph * 1e3, 4),
+        "unique_bytes_per_step": int(uniq), "logical_bytes_per_step": int(logical),
+        "graph_unique_gbs": round(gbs_graph, 2), "logical_gbs": round(logical / t_step / 1e9, 2),
+        "parity": par,
+        "roofline": {"bound": "hbm", "achieved": round(gbs_graph, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs_graph / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(sample_bytes / statistics.median(ctimes) / 1e9, 3), "unit": "GB/s",
+                         "cores": cores, "kind": "port",
+                         "sample": f"layer 0, 4 sequences ({sum(k.shape[0] for k in ks)} tokens): gather + fp32 SDPA, median of 3",
+                         "cpu_model": cpu_model()},
+    }
+    print(json.dumps(result), flush=True)
+
+
+def step36_parity(loop, layers, nseq):
+    """The step's decode output of ``nseq`` sequences in each of ``layers`` against the
+    oracle's attention over the same pages (read back), and the step's appended K/V in place."""
+    import numpy as np
+    import torch
+    from oracle import kv_ref
+    m = loop.mgr
+    worst, ok = 0.0, True
+    for layer in layers:
+        cache = m.kv_cache[layer]
+        for r in range(nseq):
+            sid = loop.ids[r]
+            n = m._npages[sid]
+            pages = m._table[m.batch_to_seq_len[sid], :n].long()
+            L = m._seq_len(sid)
+            kv = cache[pages].float().cpu().numpy()  # [n, 2, ps, hkv, d]
+            k = kv[:, 0].reshape(-1, loop.hkv, loop.d)[:L]
+            v = kv[:, 1].reshape(-1, loop.hkv, loop.d)[:L]
+            # the appended token sits at position L - 1, bit for bit
+            ok &= bool(torch.equal(cache[pages[(L - 1) // 16], 0, (L - 1) % 16].cpu(), loop.k[layer, r].cpu()))
+            ok &= bool(torch.equal(cache[pages[(L - 1) // 16], 1, (L - 1) % 16].cpu(), loop.v[layer, r].cpu()))
+            q = loop.q[layer, r:r + 1].float().cpu().numpy().astype(np.float64)
+            ref = kv_ref._attend(q, k, v, [L], loop.d ** -0.5)[0]
+            got = loop.out[layer, r].float().cpu().numpy()
+            err = np.abs(got - ref)
+            ok &= bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
+            worst = max(worst, float(err.max()))
+    return {"max_abs_err": worst, "within_atol2e-3_rtol1e-2_and_append_bitexact": ok}
+
+
 def chunked_prefill(args, torch, workloads, ops, dev):
     """Chunked prefill at Qwen2.5-3B shape: append each request's chunk, then causal ragged
     attention over prefix + chunk.  FLOPs count valid causal (query, key) pairs only:
@@ -316,11 +442,14 @@ def main():
     ap.add_argument("--ctas", type=int, default=None, help="decode workgroups (default: one per CU)")
     ap.add_argument("--dynamic", action="store_true",
                     help="waves take pages on demand (faster, not bitwise reproducible)")
-    ap.add_argument("--workload", default="qwen25_3b_b64", choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill"],
+    ap.add_argument("--workload", default="qwen25_3b_b64",
+                    choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill", "qwen25_3b_step36"],
                     help="qwen25_3b_b64: the headline decode + append step (default); llama31_8b_b128: "
                          "long-context decode at Llama-3.1-8B shape, B=128, ~4.4 GB of K/V in a 20 GB pool "
                          "(decode only, generated on the device); qwen25_3b_prefill: chunked prefill, 8 "
-                         "requests x 512-token chunks onto prefixes U[0, 8192] (the matrix-core roofline)")
+                         "requests x 512-token chunks onto prefixes U[0, 8192] (the matrix-core roofline); "
+                         "qwen25_3b_step36: the 36-layer graph-captured decode step, B=128, on a shared "
+                         "2048-token prefix with pages allocated and freed by the device pool")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="for counter runs: N eager decode and append launches, then N plain "
                          "copies of the decode's byte count (the counters' calibration), then exit")
@@ -341,6 +470,8 @@ def main():
         return long_context(args, torch, workloads, BatchDecodeWithPagedKVCacheWrapper, dev)
     if args.workload == "qwen25_3b_prefill":
         return chunked_prefill(args, torch, workloads, ops, dev)
+    if args.workload == "qwen25_3b_step36":
+        return step36(args, torch, workloads, dev)
     print("bench: building Qwen2.5-3B B=64 decode batch", file=sys.stderr, flush=True)
     wb = workloads.qwen25_3b_decode()
     NL = args.layers

@@ -11,7 +11,9 @@
 // ids never leave the device.  Operations are queued on the host and applied here in one
 // launch, in their original order.
 //
-//   pkv_pool_apply   <- allocate / append_tokens / free / init_cuda_graph_buffers
+//   pkv_pool_apply   <- allocate / append_tokens / free / init_cuda_graph_buffers, and the
+//                       shared-prefix extension (a sequence's row starts with a copy of the
+//                       prefix's full pages; no counterpart in the reference)
 //   pkv_pool_gather  <- get_append_metadata / fill_cuda_graph_metadata (the page walk that
 //                       builds kv_indices, manager.py:124-133, 231-246)
 #include "common.h"
@@ -25,6 +27,7 @@ namespace {
 // push of the same batch wrote).  Operation i is ops[5i .. 5i+4] = {kind, row, pos, col, n}:
 //   kind 0, pop:  table[row][col + k] = stack[pos - 1 - k]   (k < n: the order of pop())
 //   kind 1, push: stack[pos + k] = table[row][col + k]       (the order of extend())
+//   kind 2, copy: table[row][col + k] = table[pos][k]         (pos = the prefix's row)
 // Operations that fall outside the stack or the table are skipped and counted in *err.
 __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
                                   int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err) {
@@ -33,16 +36,19 @@ __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* t
     if (threadIdx.x < 5) s_op[threadIdx.x] = ops[5 * i + threadIdx.x];
     __syncthreads();
     const int kind = s_op[0], row = s_op[1], pos = s_op[2], col = s_op[3], n = s_op[4];
-    const bool ok = (kind == 0 || kind == 1) && row >= 0 && row < rows && col >= 0 && n >= 0 &&
-                    (int64_t)col + n <= stride &&
-                    (kind == 0 ? (pos - n >= 0 && pos <= stack_size) : (pos >= 0 && pos + n <= stack_size));
+    bool ok = kind >= 0 && kind <= 2 && row >= 0 && row < rows && col >= 0 && n >= 0 && (int64_t)col + n <= stride;
+    if (kind == 0) ok = ok && pos - n >= 0 && pos <= stack_size;
+    else if (kind == 1) ok = ok && pos >= 0 && pos + n <= stack_size;
+    else ok = ok && pos >= 0 && pos < rows && pos != row && n <= stride;
     if (!ok) {
       if (threadIdx.x == 0 && err) atomicAdd(err, 1);
     } else {
       int32_t* trow = table + (int64_t)row * stride + col;
+      const int32_t* src = table + (int64_t)pos * stride;  // (kind 2 only)
       for (int k = threadIdx.x; k < n; k += blockDim.x) {
         if (kind == 0) trow[k] = stack[pos - 1 - k];
-        else stack[pos + k] = trow[k];
+        else if (kind == 1) stack[pos + k] = trow[k];
+        else trow[k] = src[k];
       }
     }
     __syncthreads();  // this operation's writes are visible to the next one

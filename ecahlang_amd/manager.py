@@ -25,6 +25,12 @@ with ``T % block_size == 0`` records ``block_size`` as the last page's length in
 (manager.py:106).  The reference's 0 makes ``get_seq_lens`` report ``T - block_size`` while
 ``T`` tokens are held; ``strict_reference_q1=True`` restores it.
 
+One extension with no counterpart in the reference (which has no page refcounting, so its
+sequences cannot share pages): ``allocate(b, T, prefix=p)`` starts sequence b's page list
+with the full pages of the live sequence p (copied on the device, not popped) and pops pages
+for the rest of its T tokens; ``free(b)`` pushes back only b's own pages, and ``free(p)``
+raises while any sequence shares p.  The oracle restates the same rules.
+
 The sampling helpers (init_sampling_buffers, fill_sampling_params,
 fill_cuda_graph_sampling_params, ``mask_penalty``) are outside the paged-KV path; they are
 kept, as plain tensor code, so that ``main.py`` finds the attributes it uses.
@@ -39,7 +45,7 @@ import torch
 from ._lib import check, lib, stream_ptr
 from .ops import append_paged_kv_cache, get_batch_indices_positions, get_seq_lens
 
-_POP, _PUSH = 0, 1
+_POP, _PUSH, _COPY = 0, 1, 2
 
 
 def get_total_free_memory(index: int = 0) -> int:
@@ -161,6 +167,8 @@ class AutoKVCacheManager:
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._ops: list = []
         self._n_padding = 0
+        self._shared: dict = {}  # batch_id -> (prefix id, leading shared pages)
+        self._refs: dict = {}    # prefix id -> live sequences sharing its pages
 
         # host bookkeeping: counts only
         self.free_seq_lens = list(range(self.seq_lens))
@@ -244,18 +252,37 @@ class AutoKVCacheManager:
 
     # ------------------------------------------------------------------ page pool (A3-A5)
 
-    def allocate(self, batch_id, total_tokens: int) -> _Pages:
-        """manager.py:99-112: pop ceil(T / block_size) pages, take a sequence slot."""
-        num_pages = math.ceil(total_tokens / self.block_size)
+    def _seq_len(self, batch_id) -> int:
+        n = self._npages[batch_id]
+        return (n - 1) * self.block_size + self.batch_to_page_lengths[batch_id] if n else 0
+
+    def allocate(self, batch_id, total_tokens: int, *, prefix=None) -> _Pages:
+        """manager.py:99-112: pop ceil(T / block_size) pages, take a sequence slot.  With
+        ``prefix`` (an extension), the full pages of that live sequence come first and only
+        the rest are popped."""
+        shared = 0
+        if prefix is not None:
+            if prefix not in self._npages:
+                raise ValueError(f"{prefix} not allocated")
+            shared = self._seq_len(prefix) // self.block_size
+            if total_tokens < shared * self.block_size:
+                raise ValueError("a sequence cannot be shorter than its shared prefix")
+        num_pages = math.ceil(total_tokens / self.block_size) - shared
         if self._n_free < num_pages:
             raise RuntimeError("Not enough KV cache blocks available")
         if not self.free_seq_lens:
             raise IndexError("pop from empty list")
         slot = self.free_seq_lens.pop()
-        self._ensure_stride(num_pages)
+        self._ensure_stride(shared + num_pages)
+        if prefix is not None:  # (a prefix with no full page yet is still held)
+            self._shared[batch_id] = (prefix, shared)
+            self._refs[prefix] = self._refs.get(prefix, 0) + 1
+        if shared:
+            self._ops.append((_COPY, slot, self.batch_to_seq_len[prefix], 0, shared))
         if num_pages:
-            self._ops.append((_POP, slot, self._n_free, 0, num_pages))
+            self._ops.append((_POP, slot, self._n_free, shared, num_pages))
             self._n_free -= num_pages
+        num_pages += shared
         self._npages[batch_id] = num_pages
         page_len = total_tokens % self.block_size
         if page_len == 0 and total_tokens > 0 and not self.strict_reference_q1:
@@ -267,13 +294,19 @@ class AutoKVCacheManager:
         return _Pages(self, slot, num_pages)
 
     def free(self, batch_id) -> None:
-        """manager.py:114-120: push the pages back in page order, release the slot."""
+        """manager.py:114-120: push the pages back in page order, release the slot (a
+        sequence's shared prefix pages stay with the prefix)."""
+        if self._refs.get(batch_id):
+            raise RuntimeError(f"{batch_id} is the shared prefix of {self._refs[batch_id]} live sequences")
         n = self._npages.pop(batch_id, 0)
         self.batch_to_page_lengths.pop(batch_id, None)
         slot = self.batch_to_seq_len.pop(batch_id, None)
-        if n and slot is not None:
-            self._ops.append((_PUSH, slot, self._n_free, 0, n))
-            self._n_free += n
+        prefix, shared = self._shared.pop(batch_id, (None, 0))
+        if prefix is not None:
+            self._refs[prefix] -= 1
+        if n > shared and slot is not None:
+            self._ops.append((_PUSH, slot, self._n_free, shared, n - shared))
+            self._n_free += n - shared
         if slot is not None:
             self.free_seq_lens.append(slot)
 
@@ -348,9 +381,11 @@ class AutoKVCacheManager:
 
     # ------------------------------------------------------------------ CUDA-graph buckets (A10-A12)
 
-    def init_cuda_graph_buffers(self, bucket_sizes) -> None:
+    def init_cuda_graph_buffers(self, bucket_sizes, *, max_indices: int | None = None) -> None:
         """manager.py:207-226: reserve max(bucket) padding pages and the static per-bucket
-        buffers the captured step reads."""
+        buffers the captured step reads.  ``max_indices`` (an extension) sizes the static
+        ``kv_indices`` buffers; the reference's ``max_blocks`` is too small once sequences
+        share prefix pages (a shared page appears in every table that holds it)."""
         max_bucket = max(bucket_sizes)
         if self._n_free < max_bucket:
             raise RuntimeError(f"Not enough free blocks for {max_bucket} padding pages")
@@ -361,7 +396,8 @@ class AutoKVCacheManager:
         dev = self.device
         self._cg_temperature, self._cg_top_k, self._cg_top_p = {}, {}, {}
         for bs in bucket_sizes:
-            self._cg_kv_indices[bs] = torch.zeros(self.max_blocks, dtype=torch.int32, device=dev)
+            self._cg_kv_indices[bs] = torch.zeros(max(self.max_blocks, max_indices or 0), dtype=torch.int32,
+                                                  device=dev)
             self._cg_kv_indptr[bs] = torch.zeros(bs + 1, dtype=torch.int32, device=dev)
             self._cg_kv_last_page_len[bs] = torch.zeros(bs, dtype=torch.int32, device=dev)
             self._cg_batch_indices[bs] = torch.arange(bs, dtype=torch.int32, device=dev)

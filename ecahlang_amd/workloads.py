@@ -205,3 +205,156 @@ def llama31_8b_decode_device(device, seed=1004, batch=128, lo=1024, hi=32768,
     page_bytes = 2 * 16 * 8 * 128 * 2
     return device_decode_batch([c + 1 for c in ctx], 32, 8, 128, torch.bfloat16, seed,
                                pool_bytes // page_bytes, device)
+
+
+class SharedPrefixDecodeLoop:
+    """Repeated decode steps of every layer of a model over one page pool, driven through
+    AutoKVCacheManager and the decode wrapper the way the serving loop drives them
+    (ecahlang/main.py:320-381): per step, ``append_tokens(b, 1)`` for every sequence (a page is
+    popped on the device when the last one fills), ``fill_cuda_graph_metadata`` for the
+    batch's bucket, ``plan``, then one graph replay of every layer's append + decode.
+
+    Every sequence starts with the full pages of one shared prefix (``allocate(...,
+    prefix=)``), followed by pages of its own.  ``retire`` frees ``finish`` randomly chosen
+    sequences (their own pages go back to the pool; the prefix's stay) and starts as many new
+    ones on the same prefix, whose tokens are written into their pages as a prefill would
+    leave them.  Default shape: Qwen2.5-3B attention (36 layers, 16 q / 2 kv heads, head_dim
+    128, fp16), batch 128, a 2048-token prefix and own suffixes of U[64, 1024] tokens.
+
+    Values are N(0,1)*scale from a device generator; every slot no token owns is NaN.  Lengths
+    and the finished sequences come from a host generator, and every pool operation is logged
+    in ``log`` (so a test can replay it on the oracle's pool)."""
+
+    def __init__(self, device, *, layers=36, batch=128, hq=16, hkv=2, d=128, dtype=torch.float16,
+                 prefix_tokens=2048, suffix=(64, 1024), finish=8, max_steps=64, seed=1005, scale=0.5):
+        from .manager import AutoKVCacheManager
+        from .wrappers import BatchDecodeWithPagedKVCacheWrapper
+
+        self.device = torch.device(device)
+        self.layers, self.batch, self.hq, self.hkv, self.d, self.dtype = layers, batch, hq, hkv, d, dtype
+        self.ps = 16
+        self.prefix_tokens, self.suffix, self.finish, self.scale = prefix_tokens, suffix, finish, scale
+        self.gen = torch.Generator().manual_seed(seed + 7919)
+        self.dgen = torch.Generator(device=self.device).manual_seed(seed)
+        es = torch.tensor([], dtype=dtype).element_size()
+        self.page_bytes = 2 * self.ps * hkv * d * es  # one page of one layer
+        own_max = -(-(suffix[1] + max_steps + 1) // self.ps)
+        pool = int(math.ceil(1.25 * (-(-prefix_tokens // self.ps) + batch * own_max))) + batch
+        self.mgr = AutoKVCacheManager(layers, hkv, d, dtype=dtype, device=self.device,
+                                      total_gpu_mem_bytes=pool * layers * self.page_bytes, mem_utilization=1.0,
+                                      max_pages_per_seq=-(-prefix_tokens // self.ps) + own_max,
+                                      seq_lens=max(128, batch + 1))
+        self.mgr.kv_cache.fill_(float("nan"))
+        self.log: list = []
+        self.stream = torch.cuda.Stream(device=self.device)
+        with torch.cuda.stream(self.stream):
+            self.mgr.allocate("prefix", prefix_tokens)
+            self.log.append(("allocate", "prefix", prefix_tokens, None))
+            self._write_tokens("prefix", 0)
+            self.ids = []
+            self._next_id = 0
+            for _ in range(batch):
+                self.ids.append(self._start_sequence())
+            self.mgr.init_cuda_graph_buffers([batch], max_indices=batch * self.mgr._stride)
+            self.log.append(("init_cuda_graph_buffers", [batch]))
+            shape = (layers, batch)
+            self.q = self._randn(shape + (hq, d))
+            self.k = self._randn(shape + (hkv, d))
+            self.v = self._randn(shape + (hkv, d))
+            self.out = torch.empty_like(self.q)
+            self.wrapper = BatchDecodeWithPagedKVCacheWrapper(
+                torch.empty(128 << 20, dtype=torch.uint8, device=self.device), "NHD")
+        self.graph = None
+
+    # ---------------------------------------------------------------- synthetic contents
+    def _randn(self, shape):
+        return (torch.randn(shape, generator=self.dgen, device=self.device, dtype=torch.float32)
+                * self.scale).to(self.dtype)
+
+    def _write_tokens(self, sid, first_page: int) -> None:
+        """Fill sequence sid's pages from first_page on (every layer) with fresh values; the
+        slots past its last token stay NaN."""
+        m = self.mgr
+        m._flush()
+        n = m._npages[sid]
+        if n <= first_page:
+            return
+        pages = m._table[m.batch_to_seq_len[sid], first_page:n].long()
+        cache = m.kv_cache
+        cache[:, pages] = self._randn((self.layers, n - first_page, 2, self.ps, self.hkv, self.d))
+        last = m.batch_to_page_lengths[sid]
+        if last < self.ps:
+            cache[:, pages[-1:], :, last:] = float("nan")
+
+    def _start_sequence(self):
+        sid = f"s{self._next_id}"
+        self._next_id += 1
+        lo, hi = self.suffix
+        n = int(torch.randint(lo, hi + 1, (1,), generator=self.gen))
+        tokens = self.prefix_tokens + n
+        self.mgr.allocate(sid, tokens, prefix="prefix")
+        self.log.append(("allocate", sid, tokens, "prefix"))
+        self._write_tokens(sid, self.mgr._shared[sid][1])
+        return sid
+
+    # ---------------------------------------------------------------- one step
+    def begin_step(self) -> None:
+        """Host bookkeeping and device metadata for one decode step (main.py:328-347)."""
+        m = self.mgr
+        with torch.cuda.stream(self.stream):
+            for sid in self.ids:
+                m.append_tokens(sid, 1)
+                self.log.append(("append_tokens", sid, 1))
+            m.fill_cuda_graph_metadata(self.batch, self.ids)
+            self.log.append(("fill_cuda_graph_metadata", self.batch, list(self.ids)))
+            self.wrapper.plan(m._cg_kv_indptr[self.batch], m._cg_kv_indices[self.batch],
+                              m._cg_kv_last_page_len[self.batch], self.hq, self.hkv, self.d, self.ps,
+                              pos_encoding_mode="NONE", q_data_type=self.dtype)
+
+    def layers_fn(self) -> None:
+        """Every layer's append of the step's token and its decode (what the graph holds)."""
+        m = self.mgr
+        for layer in range(self.layers):
+            m.append_paged_kv_cache_cuda_graph(self.k[layer], self.v[layer], self.batch, layer)
+            self.wrapper.run(self.q[layer], m.kv_cache[layer], out=self.out[layer])
+
+    def replay(self) -> None:
+        """Run the step's layers from the captured graph (captured on the first call, after
+        an eager warm-up: a repeated append writes the same values to the same slots)."""
+        with torch.cuda.stream(self.stream):
+            if self.graph is None:
+                self.layers_fn()
+                self.stream.synchronize()
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph, stream=self.stream):
+                    self.layers_fn()
+            self.graph.replay()
+
+    def retire(self) -> list:
+        """Finish ``finish`` random sequences and start new ones in their batch rows."""
+        with torch.cuda.stream(self.stream):
+            rows = torch.randperm(self.batch, generator=self.gen)[: self.finish].tolist()
+            for r in sorted(rows):
+                self.mgr.free(self.ids[r])
+                self.log.append(("free", self.ids[r]))
+                self.ids[r] = self._start_sequence()
+        return rows
+
+    def new_inputs(self) -> None:
+        with torch.cuda.stream(self.stream):
+            for t in (self.q, self.k, self.v):
+                t.copy_(self._randn(t.shape))
+
+    # ---------------------------------------------------------------- accounting
+    def seq_lens(self) -> list:
+        return [self.mgr._seq_len(s) for s in self.ids]
+
+    def step_bytes(self) -> dict:
+        """Bytes one step's attention reads and writes per layer: ``unique`` counts every
+        distinct valid token once (the shared prefix once), ``logical`` once per sequence."""
+        es = torch.tensor([], dtype=self.dtype).element_size()
+        tok = 2 * self.hkv * self.d * es
+        lens = self.seq_lens()
+        io = 2 * self.batch * self.hq * self.d * es + self.batch * tok  # q in, o out, appended K/V
+        unique = (self.prefix_tokens + sum(L - self.prefix_tokens for L in lens)) * tok + io
+        return {"unique": unique, "logical": sum(lens) * tok + io}

@@ -151,6 +151,9 @@ int pkv_batch_prefill_mfma(const void* q, int64_t q_stride_n, int64_t q_stride_h
  *   kind 0, pop  (allocate :104, append_tokens :201-203, init_cuda_graph_buffers :212):
  *     table[row][col + k] = stack[pos - 1 - k] for k < n
  *   kind 1, push (free :116): stack[pos + k] = table[row][col + k] for k < n
+ *   kind 2, copy: table[row][col + k] = table[pos][k] for k < n (a sequence that shares the
+ *     full pages of a prefix sequence in row pos; the reference has no prefix sharing, so this
+ *     kind has no counterpart there)
  * Operations outside the stack or table are skipped and counted in *err (may be NULL). */
 int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
                    int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err, void* stream);

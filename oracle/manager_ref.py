@@ -8,6 +8,12 @@ One deliberate divergence, shared with the product manager: ``allocate(T)`` with
 0 (manager.py:106) makes ``get_seq_lens`` report T - block_size while T tokens are held
 (and a following append overwrites slot 0 of the last full page); block_size is the only
 value consistent with the pages it pops.  The page ids popped are unchanged.
+
+One extension with no counterpart in the reference (which has no page refcounting): prefix
+sharing.  ``allocate(b, T, prefix=p)`` gives sequence b the full pages of the live sequence p
+first (shared, not popped), then pops the pages for the rest of its T tokens; ``free(b)``
+returns only b's own pages; ``free(p)`` while sequences share p raises.  This is the
+restatement the device manager's prefix sharing is checked against.
 """
 from __future__ import annotations
 
@@ -29,14 +35,26 @@ class RefKVCacheManager:
         self.batch_to_seq_len: dict = {}
         self.padding_pages: list = []
         self.strict_reference_q1 = strict_reference_q1
+        self.shared: dict = {}  # batch_id -> (prefix id, number of leading shared pages)
+        self.refs: dict = {}    # prefix id -> live sequences sharing its pages
 
-    # manager.py:99-112
-    def allocate(self, batch_id, total_tokens: int) -> list:
-        num_pages = math.ceil(total_tokens / self.block_size)
+    # manager.py:99-112 (+ the prefix extension)
+    def allocate(self, batch_id, total_tokens: int, prefix=None) -> list:
+        shared = []
+        if prefix is not None:
+            if prefix not in self.batch_to_blocks:
+                raise ValueError(f"{prefix} not allocated")
+            shared = self.batch_to_blocks[prefix][: self.seq_len(prefix) // self.block_size]
+            if total_tokens < len(shared) * self.block_size:
+                raise ValueError("a sequence cannot be shorter than its shared prefix")
+        num_pages = math.ceil(total_tokens / self.block_size) - len(shared)
         if len(self.free_blocks) < num_pages:
             raise RuntimeError("Not enough KV cache blocks available")
-        blocks = [self.free_blocks.pop() for _ in range(num_pages)]
+        blocks = shared + [self.free_blocks.pop() for _ in range(num_pages)]
         self.batch_to_blocks[batch_id] = blocks
+        if prefix is not None:
+            self.shared[batch_id] = (prefix, len(shared))
+            self.refs[prefix] = self.refs.get(prefix, 0) + 1
         page_len = total_tokens % self.block_size
         if page_len == 0 and total_tokens > 0 and not self.strict_reference_q1:
             page_len = self.block_size
@@ -46,10 +64,15 @@ class RefKVCacheManager:
         self.batch_to_seq_len[batch_id] = seq_slot
         return blocks
 
-    # manager.py:114-120
+    # manager.py:114-120 (+ the prefix extension)
     def free(self, batch_id) -> None:
+        if self.refs.get(batch_id):
+            raise RuntimeError(f"{batch_id} is the shared prefix of {self.refs[batch_id]} live sequences")
         blocks = self.batch_to_blocks.pop(batch_id, [])
-        self.free_blocks.extend(blocks)
+        prefix, n_shared = self.shared.pop(batch_id, (None, 0))
+        if prefix is not None:
+            self.refs[prefix] -= 1
+        self.free_blocks.extend(blocks[n_shared:])
         self.batch_to_page_lengths.pop(batch_id, None)
         seq_slot = self.batch_to_seq_len.pop(batch_id, None)
         if seq_slot is not None:

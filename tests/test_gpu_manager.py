@@ -203,3 +203,51 @@ def test_end_to_end_prefill_then_decode_steps():
                 np.testing.assert_allclose(out[b], ref, atol=2e-3, rtol=1e-2,
                                            err_msg=f"step {step} layer {layer} seq {sid}")
     assert m.pool_errors() == 0
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_prefix_sharing_matches_oracle(seed):
+    """The prefix extension (allocate(..., prefix=)) against the oracle's restatement: page
+    lists, free stack and exceptions, under random allocate / share / append / free."""
+    rng = random.Random(100 + seed)
+    P = 120
+    dev, ref = _pool(P), RefKVCacheManager(P)
+    ids = list(range(10))
+    for step in range(300):
+        kind = rng.choice(["alloc", "share", "share", "append", "append", "free", "meta"])
+        sid = rng.choice(ids)
+        n = rng.choice([0, 1, 2, 15, 16, 17, 33, 70])
+        if kind == "meta":
+            live = [s for s in ids if s in ref.batch_to_blocks]
+            idx, ptr, last = dev.get_append_metadata(live)
+            assert (idx.tolist(), ptr.tolist(), last.tolist()) == tuple(map(list, ref.get_append_metadata(live)))
+            continue
+        if kind == "share":
+            live = sorted(s for s in ids if s in ref.batch_to_blocks)
+            if not live or sid in ref.batch_to_blocks:
+                continue
+            p = rng.choice(live + [99])  # 99: not allocated (ValueError in both)
+            tokens = (ref.seq_len(p) if p in ref.batch_to_blocks else 0) + rng.choice([-1, 0, 1, 20])
+            name, args, kw = "allocate", (sid, max(tokens, 0)), {"prefix": p}
+        elif kind == "alloc" and sid not in ref.batch_to_blocks:
+            name, args, kw = "allocate", (sid, n), {}
+        elif kind == "append":
+            name, args, kw = "append_tokens", (sid, n), {}
+        elif kind == "free":
+            name, args, kw = "free", (sid,), {}
+        else:
+            continue
+        err_ref = err_dev = None
+        try:
+            getattr(ref, name)(*args, **kw)
+        except (RuntimeError, ValueError) as e:
+            err_ref = (type(e), str(e))
+        try:
+            getattr(dev, name)(*args, **kw)
+        except (RuntimeError, ValueError) as e:
+            err_dev = (type(e), str(e))
+        assert err_dev == err_ref, (step, name, args, kw)
+        if step % 10 == 0 or err_ref:
+            _same_state(dev, ref)
+    _same_state(dev, ref)
+    assert dev.pool_errors() == 0

@@ -1,0 +1,104 @@
+"""The multi-layer decode step over a shared prefix (workloads.SharedPrefixDecodeLoop):
+page tables from the device pool against the oracle's pool replaying the same operations
+(prefix sharing, per-step appends with on-device page pops, frees and refills), every
+layer's appended K/V in place bit for bit, and the graph-replayed decode outputs against the
+oracle's attention over the pages read back."""
+import numpy as np
+import pytest
+import torch
+
+from ecahlang_amd import workloads
+from oracle import kv_ref
+from oracle.manager_ref import RefKVCacheManager
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _replay_log(loop, ref, start):
+    """Apply loop.log[start:] to the oracle pool; return the last graph metadata it built."""
+    meta = None
+    for op in loop.log[start:]:
+        if op[0] == "allocate":
+            ref.allocate(op[1], op[2], prefix=op[3])
+        elif op[0] == "append_tokens":
+            ref.append_tokens(op[1], op[2])
+        elif op[0] == "free":
+            ref.free(op[1])
+        elif op[0] == "init_cuda_graph_buffers":
+            ref.init_cuda_graph_buffers(op[1])
+        elif op[0] == "fill_cuda_graph_metadata":
+            meta = ref.fill_cuda_graph_metadata(op[1], op[2])
+        else:
+            raise AssertionError(op)
+    return meta
+
+
+def _check_layer(loop, layer, rows, idx, ptr, last):
+    """Append in place (bitwise) and decode output (oracle tolerance) for batch rows."""
+    cache = loop.mgr.kv_cache[layer]
+    for r in rows:
+        pages = torch.tensor(idx[ptr[r]:ptr[r + 1]], dtype=torch.long, device=DEV)
+        L = (len(pages) - 1) * 16 + last[r]
+        p, s = pages[(L - 1) // 16], (L - 1) % 16
+        assert torch.equal(cache[p, 0, s], loop.k[layer, r]), (layer, r)
+        assert torch.equal(cache[p, 1, s], loop.v[layer, r]), (layer, r)
+        kv = cache[pages].float().cpu().numpy()
+        k = kv[:, 0].reshape(-1, loop.hkv, loop.d)[:L]
+        v = kv[:, 1].reshape(-1, loop.hkv, loop.d)[:L]
+        q = loop.q[layer, r:r + 1].float().cpu().numpy().astype(np.float64)
+        ref = kv_ref._attend(q, k, v, [L], loop.d ** -0.5)[0]
+        got = loop.out[layer, r].float().cpu().numpy()
+        np.testing.assert_allclose(got, ref, atol=2e-3, rtol=1e-2, err_msg=f"layer {layer} row {r}")
+
+
+def test_small_loop_matches_oracle_every_step():
+    loop = workloads.SharedPrefixDecodeLoop(DEV, layers=3, batch=16, prefix_tokens=256, suffix=(1, 200),
+                                            finish=4, max_steps=12, seed=7)
+    ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
+    done = 0
+    for step in range(8):
+        print(f"small loop step {step}", flush=True)
+        loop.new_inputs()
+        loop.begin_step()
+        loop.replay()
+        torch.cuda.synchronize()
+        idx, ptr, last, pos = _replay_log(loop, ref, done)
+        done = len(loop.log)
+        b = loop.batch
+        assert loop.mgr._cg_kv_indices[b][:len(idx)].tolist() == idx
+        assert loop.mgr._cg_kv_indptr[b].tolist() == ptr
+        assert loop.mgr._cg_kv_last_page_len[b].tolist() == last
+        assert loop.mgr._cg_positions[b].tolist() == pos
+        # every sequence starts with the prefix's 16 full pages
+        pre = ref.batch_to_blocks["prefix"][:16]
+        assert all(idx[ptr[r]:ptr[r] + 16] == pre for r in range(b))
+        for layer in range(loop.layers):
+            _check_layer(loop, layer, range(b), idx, ptr, last)
+        loop.retire()
+    _replay_log(loop, ref, done)
+    assert list(loop.mgr.free_blocks) == ref.free_blocks
+    assert loop.mgr.pool_errors() == 0
+
+
+def test_full_size_step_qwen_36_layers():
+    """Qwen2.5-3B attention shape, 36 layers, batch 128, 2048-token shared prefix: three steps
+    (the graph captured on the first), then layers 0, 17 and 35 checked on 8 sequences."""
+    loop = workloads.SharedPrefixDecodeLoop(DEV, max_steps=6)
+    ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
+    done = 0
+    for step in range(3):
+        print(f"full loop step {step}", flush=True)
+        loop.begin_step()
+        loop.replay()
+        torch.cuda.synchronize()
+        idx, ptr, last, pos = _replay_log(loop, ref, done)
+        done = len(loop.log)
+        assert loop.mgr._cg_kv_indptr[loop.batch].tolist() == ptr
+        assert loop.mgr._cg_kv_indices[loop.batch][:len(idx)].tolist() == idx
+        if step == 2:
+            rows = list(range(0, loop.batch, loop.batch // 8))
+            for layer in (0, 17, 35):
+                _check_layer(loop, layer, rows, idx, ptr, last)
+        loop.retire()
+    assert loop.mgr.pool_errors() == 0

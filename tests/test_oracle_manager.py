@@ -93,3 +93,70 @@ def test_seq_len_tracks_token_count():
         m.append_tokens("s", n)
         total += n
         assert m.seq_len("s") == total
+
+
+def test_prefix_sharing_hand_trace():
+    """The prefix extension on a 10-page pool, derived by hand: shared pages are the
+    prefix's full pages, never popped or pushed by the sequences that share them."""
+    m = RefKVCacheManager(10)
+    assert m.allocate("p", 40) == [9, 8, 7]           # 2 full pages + 8 tokens
+    assert m.allocate("a", 40, prefix="p") == [9, 8, 6]  # shares [9, 8]; its own page 6
+    assert m.allocate("b", 32, prefix="p") == [9, 8]     # nothing of its own yet
+    assert m.batch_to_page_lengths["b"] == 16
+    m.append_tokens("b", 1)                              # 17th token of its last page: pops 5
+    assert m.batch_to_blocks["b"] == [9, 8, 5] and m.batch_to_page_lengths["b"] == 1
+    with pytest.raises(RuntimeError, match="p is the shared prefix of 2 live sequences"):
+        m.free("p")
+    with pytest.raises(ValueError, match="q not allocated"):
+        m.allocate("c", 40, prefix="q")
+    with pytest.raises(ValueError, match="shorter than its shared prefix"):
+        m.allocate("c", 31, prefix="p")
+    with pytest.raises(RuntimeError, match="Not enough KV cache blocks available"):
+        m.allocate("c", 32 + 16 * 6, prefix="p")  # 6 own pages, 5 free
+    assert m.free_blocks == [0, 1, 2, 3, 4]
+    m.free("a")
+    assert m.free_blocks == [0, 1, 2, 3, 4, 6]
+    m.free("b")
+    m.free("p")
+    assert m.free_blocks == [0, 1, 2, 3, 4, 6, 5, 9, 8, 7]
+    # a prefix whose last page is partial shares only its full pages
+    m.allocate("p2", 20)                                  # pops 7, 8
+    assert m.allocate("d", 20, prefix="p2") == [7, 9]
+
+
+prefix_ops = st.lists(st.tuples(st.sampled_from(["alloc", "share", "append", "free"]), st.integers(0, 5),
+                                st.integers(0, 70)), max_size=60)
+
+
+@settings(max_examples=200, deadline=None)
+@given(prefix_ops)
+def test_prefix_pool_invariants(seq):
+    P = 60
+    m = RefKVCacheManager(P)
+    for kind, sid, n in seq:
+        try:
+            if kind == "alloc" and sid not in m.batch_to_blocks:
+                m.allocate(sid, n)
+            elif kind == "share" and sid not in m.batch_to_blocks:
+                live = sorted(m.batch_to_blocks)
+                if live:
+                    p = live[n % len(live)]
+                    m.allocate(sid, m.seq_len(p) + n % 20, prefix=p)
+            elif kind == "append" and sid in m.batch_to_blocks:
+                m.append_tokens(sid, n)
+            elif kind == "free":
+                m.free(sid)
+        except RuntimeError:
+            pass
+        own = {b: pages[m.shared.get(b, (None, 0))[1]:] for b, pages in m.batch_to_blocks.items()}
+        flat = [p for pages in own.values() for p in pages]
+        # own pages are disjoint and conserved with the free list
+        assert len(flat) == len(set(flat))
+        assert sorted(flat + m.free_blocks) == list(range(P))
+        for b, (p, k) in m.shared.items():
+            # shared pages are the prefix's own leading pages, and the prefix is live
+            assert m.batch_to_blocks[b][:k] == m.batch_to_blocks[p][:k]
+            assert m.refs[p] >= 1
+        for b, pages in m.batch_to_blocks.items():
+            if pages:
+                assert m.seq_len(b) == (len(pages) - 1) * 16 + m.batch_to_page_lengths[b]
