@@ -186,6 +186,10 @@ class AutoKVCacheManager:
         self._cg_batch_indices: dict = {}
         self._cg_positions: dict = {}
         self._cg_append_indptr: dict = {}
+        # The pool's initial state (free stack, page table, cache) is written on the current
+        # stream; a caller may go on to drive the pool from another stream, so it is complete
+        # before the constructor returns.
+        torch.cuda.current_stream(self.device).synchronize()
 
     # ------------------------------------------------------------------ device pool plumbing
 

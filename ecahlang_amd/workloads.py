@@ -247,6 +247,9 @@ class SharedPrefixDecodeLoop:
         self.mgr.kv_cache.fill_(float("nan"))
         self.log: list = []
         self.stream = torch.cuda.Stream(device=self.device)
+        # the pool's tensors were initialised on the current stream; everything below runs on
+        # self.stream
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(self.stream):
             self.mgr.allocate("prefix", prefix_tokens)
             self.log.append(("allocate", "prefix", prefix_tokens, None))
