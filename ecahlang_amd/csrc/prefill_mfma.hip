@@ -8,7 +8,7 @@
 //   item = (request, KV head, 256 / g query tokens, a chunk [k0, k1) of the keys they see)
 // A workgroup of 8 waves owns the item's 256 query rows (row r = token r / g, head r % g of the
 // KV head's group), so every staged K/V page serves all 256 rows.  Per 64 keys (four pages),
-// staged in LDS by all threads and double-buffered:
+// staged in LDS by all threads in a ring of three stages:
 //   S^T[key][row] = K . Q^T      v_mfma_f32_16x16x32, A = K from LDS, B = Q in registers
 //   online softmax per row in the accumulator layout (lane = row l % 16, keys 4*(l/16) + i)
 //   O^T[dim][row] += V^T . P     v_mfma_f32_16x16x32 over two pages at a time: the reduction
