@@ -17,6 +17,9 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+// 16 bytes as a plain vector (arrays of it stay in registers; arrays of the uint4 struct copied
+// to and from memory may be left in scratch)
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 template <typename To, typename From>
 __device__ __forceinline__ To bitcast_(const From& x) {
@@ -34,9 +37,10 @@ template <> struct Mma<_Float16> {
   static __device__ __forceinline__ f4 pv(uint2 a, uint2 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast_<h4>(a), bitcast_<h4>(b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float x, float y) {
-    _Float16 a = (_Float16)x, b = (_Float16)y;
-    return (uint32_t)bitcast_<uint16_t>(a) | ((uint32_t)bitcast_<uint16_t>(b) << 16);
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {  // v_cvt_pk_f16_f32
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return bitcast_<uint32_t>(__builtin_convertvector((f2{x, y}), h2));
   }
 };
 template <> struct Mma<__hip_bfloat16> {
@@ -46,9 +50,10 @@ template <> struct Mma<__hip_bfloat16> {
   static __device__ __forceinline__ f4 pv(uint2 a, uint2 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bitcast_<s4>(a), bitcast_<s4>(b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float x, float y) {
-    __hip_bfloat16 a = __float2bfloat16(x), b = __float2bfloat16(y);
-    return (uint32_t)bitcast_<uint16_t>(a) | ((uint32_t)bitcast_<uint16_t>(b) << 16);
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {  // v_cvt_pk_bf16_f32
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return bitcast_<uint32_t>(__builtin_convertvector((f2{x, y}), b2));
   }
 };
 
@@ -59,6 +64,15 @@ template <> struct Mma<__hip_bfloat16> {
 template <int D>
 __device__ __forceinline__ int vswz(int t) {
   return D == 128 ? 2 * (t & 7) : 2 * ((t >> 1) & 3);
+}
+
+// Chunk swizzle of a staged K tile: 16-byte chunk c of key row t lives at c ^ kswz(t).  The
+// A-operand read (16 keys, one chunk per 16-lane group) then touches 16 distinct 16-byte bank
+// groups: rows are 256 B (D = 128: one full bank cycle per row, so XOR by t) or 128 B (D = 64:
+// row parity picks the half, XOR by t / 2 within it).
+template <int D>
+__device__ __forceinline__ int kswz(int t) {
+  return D == 128 ? (t & 15) : ((t >> 1) & 7);
 }
 
 typedef short s4v __attribute__((ext_vector_type(4)));

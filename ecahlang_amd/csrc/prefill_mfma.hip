@@ -32,6 +32,10 @@ namespace {
 constexpr int kRows = 256;   // query rows per item (8 waves x 32)
 constexpr int kStepPages = 4;  // pages (16 keys each) staged per step; chunks start at multiples of 64 keys
 constexpr int kMaxChunk = 8192;  // keys per item (its page ids are staged in LDS)
+// Lazy running max (log2 units): a row's reference max moves only when its scores exceed it by
+// more than this, so probabilities stay <= 2^kLazyMax (exact enough in fp16 / bf16 P, and far
+// from fp32 overflow in the sums) and the output rows are rescaled only on such jumps.
+constexpr float kLazyMax = 8.f;
 
 // Source of the value rows that must read as zero (past the chunk, absent pages): P is 0 there,
 // and 0 * NaN would poison P.V.
@@ -72,13 +76,6 @@ struct PrefillMfmaParams {
   float* part_o;    // [slot][kRows][D]
   int32_t o_vec;
 };
-
-// K staged row-major, 16-byte chunk c of key row t at c ^ kswz(t): the A-operand read (16 keys,
-// one chunk per 16-lane group) then touches distinct banks.
-template <int D>
-__device__ __forceinline__ int kswz(int t) {
-  return D == 128 ? (t & 15) : (t & 7);
-}
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) {
@@ -200,6 +197,16 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     lim[rt] = rtok[rt] < tq ? l : -1;
   }
 
+  // the smallest key limit among this wave's rows that exist: a step entirely below it (and
+  // with no absent page) needs no masking
+  int lim_min = INT_MAX;
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) lim_min = min(lim_min, rtok[rt] < tq ? lim[rt] : INT_MAX);
+#pragma unroll
+  for (int x = 1; x < 64; x <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, x, 64));
+  lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+  const float scale = P.scale_log2;
+
   // step st: compute on stage (ks, vs) = stage st % 3, refill stage (kn, vn) with step st + 2
   auto do_step = [&](int st, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
     // this wave's loads of step st are done (step st + 1's may still be in flight) ...
@@ -211,8 +218,12 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     if (st + 2 < nsteps) issue_step(st + 2, kn, vn);
     const int kb = k0 + 16 * NP * st;
     bool absent[NP];
+    bool full = kb + 16 * NP <= lim_min;  // (uniform)
 #pragma unroll
-    for (int kt = 0; kt < NP; ++kt) absent[kt] = page_of(kb + 16 * kt) < 0;
+    for (int kt = 0; kt < NP; ++kt) {
+      absent[kt] = page_of(kb + 16 * kt) < 0;
+      full = full && !absent[kt];
+    }
     // S^T tiles: [key tile kt][row tile rt]
     f4 sacc[NP][2];
 #pragma unroll
@@ -227,43 +238,55 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
         for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = Mma<T>::qk(a, qr[rt][s], sacc[kt][rt]);
       }
     }
-    // masked online softmax per row tile; P packed as the B operand of the P.V product
+    // online softmax per row tile on the raw scores (the scale is folded into the exponent's
+    // FMA; it is positive, so maxima commute with it); P packed as the B operand of P.V
     uint2 pb[NP][2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float sv[NP][4];
       float cmax = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int kt = 0; kt < NP; ++kt) {
+        for (int kt = 0; kt < NP; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb + 16 * kt + 4 * lg + i;
-          sv[kt][i] = (key < lim[rt] && !absent[kt]) ? sacc[kt][rt][i] * P.scale_log2 : -INFINITY;
-          cmax = fmaxf(cmax, sv[kt][i]);
-        }
+          for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[kt][rt][i];
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < NP; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb + 16 * kt + 4 * lg + i;
+            sv[kt][i] = (key < lim[rt] && !absent[kt]) ? sacc[kt][rt][i] : -INFINITY;
+          }
       }
+#pragma unroll
+      for (int kt = 0; kt < NP; ++kt)
+        cmax = fmaxf(cmax, fmaxf(fmaxf(sv[kt][0], sv[kt][1]), fmaxf(sv[kt][2], sv[kt][3])));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-      const float mnew = fmaxf(m[rt], cmax);
-      const float muse = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(m[rt] - muse);
+      const float cms = cmax * scale;
+      const bool grow = cms > m[rt] + kLazyMax;  // (false while every score so far is masked)
+      if (__ballot(grow)) {
+        const float mnew = grow ? cms : m[rt];
+        const float alpha = __builtin_amdgcn_exp2f(m[rt] - mnew);  // 0 from -inf, 1 if unchanged
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[rt][mt] *= alpha;
+        lsum[rt] *= alpha;
+        m[rt] = mnew;
+      }
+      const float nmuse = m[rt] == -INFINITY ? 0.f : -m[rt];
       float psum = 0.f;
 #pragma unroll
       for (int kt = 0; kt < NP; ++kt) {
         float pr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pr[i] = __builtin_amdgcn_exp2f(sv[kt][i] - muse);
+          pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kt][i], scale, nmuse));
           psum += pr[i];
         }
         pb[kt][rt] = make_uint2(Mma<T>::pack(pr[0], pr[1]), Mma<T>::pack(pr[2], pr[3]));
       }
-      lsum[rt] = lsum[rt] * alpha + psum;
-      if (__ballot(mnew != m[rt])) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) o[rt][mt] *= alpha;
-      }
-      m[rt] = mnew;
+      lsum[rt] += psum;
     }
     // O^T += V^T . P, two pages per 16x16x32 product
     const int tr_row = 4 * lg + (lr >> 2);
