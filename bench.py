@@ -162,6 +162,11 @@ def step36(args, torch, workloads, dev):
         loop.replay()
         loop.retire()
     torch.cuda.synchronize()
+    # a cyclic-garbage pass of the interpreter over everything torch has loaded can stall one
+    # step's host bookkeeping by tens of ms; collect once and freeze the survivors first
+    import gc
+    gc.collect()
+    gc.freeze()
     times, byts = [], []
     for _ in range(steps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

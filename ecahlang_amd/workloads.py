@@ -222,11 +222,12 @@ class SharedPrefixDecodeLoop:
     128, fp16), batch 128, a 2048-token prefix and own suffixes of U[64, 1024] tokens.
 
     Values are N(0,1)*scale from a device generator; every slot no token owns is NaN.  Lengths
-    and the finished sequences come from a host generator, and every pool operation is logged
-    in ``log`` (so a test can replay it on the oracle's pool)."""
+    and the finished sequences come from a host generator.  With ``record=True`` every pool
+    operation is logged in ``log`` (so a test can replay it on the oracle's pool)."""
 
     def __init__(self, device, *, layers=36, batch=128, hq=16, hkv=2, d=128, dtype=torch.float16,
-                 prefix_tokens=2048, suffix=(64, 1024), finish=8, max_steps=64, seed=1005, scale=0.5):
+                 prefix_tokens=2048, suffix=(64, 1024), finish=8, max_steps=64, seed=1005, scale=0.5,
+                 record=False):
         from .manager import AutoKVCacheManager
         from .wrappers import BatchDecodeWithPagedKVCacheWrapper
 
@@ -246,20 +247,21 @@ class SharedPrefixDecodeLoop:
                                       seq_lens=max(128, batch + 1))
         self.mgr.kv_cache.fill_(float("nan"))
         self.log: list = []
+        self.record = record
         self.stream = torch.cuda.Stream(device=self.device)
         # the pool's tensors were initialised on the current stream; everything below runs on
         # self.stream
         self.stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(self.stream):
             self.mgr.allocate("prefix", prefix_tokens)
-            self.log.append(("allocate", "prefix", prefix_tokens, None))
+            self._note(("allocate", "prefix", prefix_tokens, None))
             self._write_tokens("prefix", 0)
             self.ids = []
             self._next_id = 0
             for _ in range(batch):
                 self.ids.append(self._start_sequence())
             self.mgr.init_cuda_graph_buffers([batch], max_indices=batch * self.mgr._stride)
-            self.log.append(("init_cuda_graph_buffers", [batch]))
+            self._note(("init_cuda_graph_buffers", [batch]))
             shape = (layers, batch)
             self.q = self._randn(shape + (hq, d))
             self.k = self._randn(shape + (hkv, d))
@@ -268,6 +270,10 @@ class SharedPrefixDecodeLoop:
             self.wrapper = BatchDecodeWithPagedKVCacheWrapper(
                 torch.empty(128 << 20, dtype=torch.uint8, device=self.device), "NHD")
         self.graph = None
+
+    def _note(self, op) -> None:
+        if self.record:
+            self.log.append(op)
 
     # ---------------------------------------------------------------- synthetic contents
     def _randn(self, shape):
@@ -296,7 +302,7 @@ class SharedPrefixDecodeLoop:
         n = int(torch.randint(lo, hi + 1, (1,), generator=self.gen))
         tokens = self.prefix_tokens + n
         self.mgr.allocate(sid, tokens, prefix="prefix")
-        self.log.append(("allocate", sid, tokens, "prefix"))
+        self._note(("allocate", sid, tokens, "prefix"))
         self._write_tokens(sid, self.mgr._shared[sid][1])
         return sid
 
@@ -307,9 +313,9 @@ class SharedPrefixDecodeLoop:
         with torch.cuda.stream(self.stream):
             for sid in self.ids:
                 m.append_tokens(sid, 1)
-                self.log.append(("append_tokens", sid, 1))
+                self._note(("append_tokens", sid, 1))
             m.fill_cuda_graph_metadata(self.batch, self.ids)
-            self.log.append(("fill_cuda_graph_metadata", self.batch, list(self.ids)))
+            self._note(("fill_cuda_graph_metadata", self.batch, list(self.ids)))
             self.wrapper.plan(m._cg_kv_indptr[self.batch], m._cg_kv_indices[self.batch],
                               m._cg_kv_last_page_len[self.batch], self.hq, self.hkv, self.d, self.ps,
                               pos_encoding_mode="NONE", q_data_type=self.dtype)
@@ -339,7 +345,7 @@ class SharedPrefixDecodeLoop:
             rows = torch.randperm(self.batch, generator=self.gen)[: self.finish].tolist()
             for r in sorted(rows):
                 self.mgr.free(self.ids[r])
-                self.log.append(("free", self.ids[r]))
+                self._note(("free", self.ids[r]))
                 self.ids[r] = self._start_sequence()
         return rows
 

@@ -54,7 +54,7 @@ def _check_layer(loop, layer, rows, idx, ptr, last):
 
 def test_small_loop_matches_oracle_every_step():
     loop = workloads.SharedPrefixDecodeLoop(DEV, layers=3, batch=16, prefix_tokens=256, suffix=(1, 200),
-                                            finish=4, max_steps=12, seed=7)
+                                            finish=4, max_steps=12, seed=7, record=True)
     ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
     done = 0
     for step in range(8):
@@ -84,7 +84,7 @@ def test_small_loop_matches_oracle_every_step():
 def test_full_size_step_qwen_36_layers():
     """Qwen2.5-3B attention shape, 36 layers, batch 128, 2048-token shared prefix: three steps
     (the graph captured on the first), then layers 0, 17 and 35 checked on 8 sequences."""
-    loop = workloads.SharedPrefixDecodeLoop(DEV, max_steps=6)
+    loop = workloads.SharedPrefixDecodeLoop(DEV, max_steps=6, record=True)
     ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
     done = 0
     for step in range(3):
