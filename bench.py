@@ -11,7 +11,8 @@ in a hipGraph and replayed, so host launch overhead does not gap the GPU.
 
 Printed JSON line:
   value           decode GB/s = algorithmic bytes per decode launch / average decode launch
-                  time (HIP events on the launch stream around back-to-back decode launches)
+                  time (HIP events on the launch stream around back-to-back graph-replayed
+                  decode launches; the median of 5 samples, each after a warm-up burst)
   roofline        the decode kernel against MI355X's 8 TB/s HBM peak
   append_mtok_s   appended tokens per second of the append kernel (nnz = batch)
   cpu_baseline    the reference's CPU path (gather pages, then torch SDPA, in fp32) on this
@@ -65,6 +66,26 @@ def measured_traffic(wb, w):
     return t.get("traffic_bytes")
 
 
+def graph_time(torch, stream, graph, reps, launches, samples=5):
+    """Seconds per launch of a captured graph of `launches` launches: HIP events around `reps`
+    back-to-back replays on `stream`, the median of `samples` samples.  Each sample follows a
+    burst of 3 untimed replays with no synchronisation in between: the first milliseconds
+    after the GPU has idled run ~10 % slow, and a sample taken then is not the kernel's rate."""
+    times = []
+    for _ in range(samples):
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                graph.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3 / (reps * launches))
+    return statistics.median(times)
+
+
 def long_context(args, torch, workloads, Wrapper, dev):
     """Decode-only timing of the long-context workload (K/V far beyond the 256 MB MALL, so
     no pool rotation is needed); the CPU baseline runs on a bounded sample of sequences."""
@@ -90,15 +111,7 @@ def long_context(args, torch, workloads, Wrapper, dev):
                 w.run(wb.q, wb.cache, out=out)
         for _ in range(max(1, args.warmup // REP)):
             g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        n = max(1, args.steps // REP)
-        e0.record(stream)
-        for _ in range(n):
-            g.replay()
-        e1.record(stream)
-    e1.synchronize()
-    t = e0.elapsed_time(e1) / 1e3 / (n * REP)
+    t = graph_time(torch, stream, g, max(1, args.steps // REP), REP)
     gbs = dbytes / t / 1e9
     # CPU baseline on a bounded sample: the reference's gather + fp32 SDPA for 4 sequences
     import torch.nn.functional as F
@@ -186,15 +199,7 @@ def step36(args, torch, workloads, dev):
         torch.cuda.synchronize()
         par = step36_parity(loop, [0, loop.layers - 1], 8)
     # the graph alone, replayed back to back (each replay repeats the same appends)
-    REP = 10
-    with torch.cuda.stream(loop.stream):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(loop.stream)
-        for _ in range(REP):
-            loop.graph.replay()
-        e1.record(loop.stream)
-    e1.synchronize()
-    t_graph = e0.elapsed_time(e1) / 1e3 / REP
+    t_graph = graph_time(torch, loop.stream, loop.graph, 4, 1)
     L = loop.layers
     t_step = float(np.mean(times))
     uniq = float(np.mean([b["unique"] for b in byts])) * L
@@ -300,7 +305,7 @@ def chunked_prefill(args, torch, workloads, ops, dev):
         return
     stream = torch.cuda.Stream(device=dev)
 
-    def timed_graph(fn, reps, n):
+    def timed_graph(fn, reps, n, samples=5):
         with torch.cuda.stream(stream):
             fn()
             torch.cuda.synchronize()
@@ -308,18 +313,10 @@ def chunked_prefill(args, torch, workloads, ops, dev):
             with torch.cuda.graph(g, stream=stream):
                 for _ in range(reps):
                     fn()
-            g.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(n):
-                g.replay()
-            e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / 1e3 / (reps * n)
+        return graph_time(torch, stream, g, n, reps, samples)
 
     t = timed_graph(lambda: w.run(dv.q, dv.cache, out=out), 10, max(1, args.steps // 10))
-    t_valu = timed_graph(lambda: w.run(dv.q, dv.cache, out=out, force_valu=True), 1, 2)
+    t_valu = timed_graph(lambda: w.run(dv.q, dv.cache, out=out, force_valu=True), 1, 1, samples=1)
     C = wb.new_len[0]
     prefix = [L - n for L, n in zip(wb.kv_len, wb.new_len)]
     flops = 4 * wb.hq * wb.d * sum(C * p + C * (C + 1) // 2 for p in prefix)
@@ -565,14 +562,14 @@ def main():
     t_steps = timed(lambda i: step_graphs[i % NL].replay(), args.steps)
     torch.cuda.synchronize()
 
-    # --- per-kernel averages (events around back-to-back launches of one kernel)
+    # --- per-kernel averages: events around back-to-back graph-replayed launches of one
+    # kernel, the median of 5 samples after a warm-up burst (the first milliseconds after the
+    # GPU has idled run ~10 % slow, so a single sample taken then is not the kernel's rate)
     n_rep = max(3, args.steps // (REP * NL))
-    dec_graph.replay()
-    t_dec = timed(lambda i: dec_graph.replay(), n_rep) / (n_rep * REP * NL)
-    app_graph.replay()
-    t_app = timed(lambda i: app_graph.replay(), n_rep) / (n_rep * REP * NL)
-    valu_graph.replay()
-    t_valu = timed(lambda i: valu_graph.replay(), 3) / (3 * NL)
+
+    t_dec = graph_time(torch, stream, dec_graph, n_rep, REP * NL)
+    t_app = graph_time(torch, stream, app_graph, n_rep, REP * NL)
+    t_valu = graph_time(torch, stream, valu_graph, 1, NL, samples=1)
     torch.cuda.synchronize()
 
     dbytes = decode_bytes(wb)
