@@ -159,6 +159,64 @@ def long_context(args, torch, workloads, Wrapper, dev):
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 
 
+def sampling(args, torch, dev):
+    """Top-k / top-p sampling of one decode step's logits at Qwen2.5-3B's vocabulary: B = 128
+    rows of 151,936 fp16 logits, top_k 50, top_p 0.9, the default device generator.  Bytes per
+    call: the logits once plus the tokens out (the kernel's further passes over a row hit the
+    caches)."""
+    from ecahlang_amd.sampling import top_k_top_p_sampling_from_logits as sample
+    B, V = 128, 151936
+    g = torch.Generator().manual_seed(1006)
+    x = (torch.randn(B, V, generator=g) * 3).half().to(dev)
+    k = torch.full((B,), 50, dtype=torch.int32, device=dev)
+    p = torch.full((B,), 0.9, dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        sample(x, k, p)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        REP = 10
+        with torch.cuda.graph(gr, stream=stream):
+            for _ in range(REP):
+                sample(x, k, p)
+    t = graph_time(torch, stream, gr, max(1, args.steps // REP), REP)
+    nbytes = B * V * 2 + B * 4
+    gbs = nbytes / t / 1e9
+    # CPU baseline: torch's sort-based top-k / top-p sampling on this host, 8 rows
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    xc = x[:8].float().cpu()
+
+    def cpu_sample(l):
+        probs = torch.softmax(l, -1)
+        vals, idx = probs.topk(50, dim=-1)
+        vals = vals / vals.sum(-1, keepdim=True)
+        c = vals.cumsum(-1)
+        vals = torch.where(c - vals >= 0.9, torch.zeros_like(vals), vals)
+        return idx.gather(-1, torch.multinomial(vals, 1))
+
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        cpu_sample(xc)
+        times.append(time.perf_counter() - t0)
+    result = {
+        "metric": "top-k/top-p sampling GB/s of logits (% HBM peak), Qwen2.5-3B vocabulary, B=128",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1)*3 logits)",
+        "config": {"workload": "top_k_top_p_sampling_from_logits, 128 x 151936 fp16 logits, top_k 50, top_p 0.9",
+                   "rows": B, "vocab": V},
+        "sampling_us": round(t * 1e6, 3), "bytes": nbytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(8 * V * 2 / statistics.median(times) / 1e9, 3), "unit": "GB/s",
+                         "cores": cores, "kind": "port",
+                         "sample": "8 rows: torch softmax + topk + cumsum nucleus + multinomial, median of 3",
+                         "cpu_model": cpu_model()},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def step36(args, torch, workloads, dev):
     """The 36-layer decode step at Qwen2.5-3B attention shape, batch 128, on a shared
     2048-token prefix (workloads.SharedPrefixDecodeLoop): per step, the host bookkeeping and
@@ -445,13 +503,15 @@ def main():
     ap.add_argument("--dynamic", action="store_true",
                     help="waves take pages on demand (faster, not bitwise reproducible)")
     ap.add_argument("--workload", default="qwen25_3b_b64",
-                    choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill", "qwen25_3b_step36"],
+                    choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill", "qwen25_3b_step36",
+                             "qwen25_3b_sampling"],
                     help="qwen25_3b_b64: the headline decode + append step (default); llama31_8b_b128: "
                          "long-context decode at Llama-3.1-8B shape, B=128, ~4.4 GB of K/V in a 20 GB pool "
                          "(decode only, generated on the device); qwen25_3b_prefill: chunked prefill, 8 "
                          "requests x 512-token chunks onto prefixes U[0, 8192] (the matrix-core roofline); "
                          "qwen25_3b_step36: the 36-layer graph-captured decode step, B=128, on a shared "
-                         "2048-token prefix with pages allocated and freed by the device pool")
+                         "2048-token prefix with pages allocated and freed by the device pool; "
+                         "qwen25_3b_sampling: top-k/top-p sampling of 128 rows of the 151,936-token vocabulary")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="for counter runs: N eager decode and append launches, then N plain "
                          "copies of the decode's byte count (the counters' calibration), then exit")
@@ -474,6 +534,8 @@ def main():
         return chunked_prefill(args, torch, workloads, ops, dev)
     if args.workload == "qwen25_3b_step36":
         return step36(args, torch, workloads, dev)
+    if args.workload == "qwen25_3b_sampling":
+        return sampling(args, torch, dev)
     print("bench: building Qwen2.5-3B B=64 decode batch", file=sys.stderr, flush=True)
     wb = workloads.qwen25_3b_decode()
     NL = args.layers

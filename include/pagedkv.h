@@ -167,6 +167,19 @@ int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t rows, const in
                     const int32_t* indptr, int32_t batch, int32_t* kv_indices, int64_t num_indices,
                     int64_t max_total, int32_t* err, void* stream);
 
+/* Top-k / top-p sampling from logits (flashinfer.sampling.top_k_top_p_sampling_from_logits at
+ * ecahlang/main.py:377-379, 400-402, 489-491, 582-584: top-k first, then top-p on the
+ * renormalised top-k distribution, deterministic=True).  logits: rows x vocab (row stride in
+ * elements, dtype PKV fp16/bf16/fp32); top_k / top_p per row, or NULL to use top_k_all /
+ * top_p_all for every row (k <= 0 or k >= vocab: no top-k filter; top_p >= 1: no top-p
+ * filter); uniform: one number in [0, 1) per row, which selects the token by inverse CDF over
+ * the kept tokens in vocabulary order (so the caller owns the random stream).  out: int32 token
+ * per row (-1 for a row with no finite logit).  Ties at a threshold are kept. */
+int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                             int32_t dtype, const int32_t* top_k, int32_t top_k_all,
+                             const float* top_p, float top_p_all, const float* uniform,
+                             int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,8 +61,7 @@ def test_flashinfer_namespace_covers_reference_call_sites():
                  "BatchPrefillWithPagedKVCacheWrapper"):
         assert callable(getattr(flashinfer, name))
     assert callable(flashinfer.page.append_paged_kv_cache)
-    with pytest.raises(AttributeError, match="paged-KV path only"):
-        flashinfer.sampling
+    assert callable(flashinfer.sampling.top_k_top_p_sampling_from_logits)
 
 
 def test_attention_hook_registers_with_transformers():
