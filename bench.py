@@ -217,6 +217,109 @@ def sampling(args, torch, dev):
     print(json.dumps(result), flush=True)
 
 
+def rope_bytes(hq, hkv, d, es) -> int:
+    """Algorithmic bytes per token of the fused rotation + append: q read and written, k and v
+    read and written into their pages, the token's cos and sin rows, batch index and position."""
+    return 2 * es * d * (hq + 2 * hkv) + 2 * es * d + 8
+
+
+def rope_append(args, torch, workloads, ops, dev):
+    """The model's rotary embedding on the new tokens fused with the append, at Qwen2.5-3B
+    shape (16 q / 2 kv heads, head_dim 128, fp16): the chunked-prefill batch (8 requests x
+    512-token chunks, 4096 tokens) and the B = 64 decode step.  Compared with the unfused
+    sequence the model and hook run today: transformers' apply_rotary_pos_emb, then the append."""
+    import numpy as np
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+    from oracle import kv_ref, rope_ref
+
+    def cos_sin(positions, d):
+        # the model's position embeddings: theta 1e6, fp32 angles, cast to the activations' dtype
+        inv = 1.0 / (1000000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+        ang = positions.float().cpu()[:, None] * inv[None]
+        emb = torch.cat((ang, ang), -1)
+        return emb.cos().half(), emb.sin().half()
+
+    stream = torch.cuda.Stream(device=dev)
+    REP = 10
+
+    def timed(fn):
+        with torch.cuda.stream(stream):
+            fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                for _ in range(REP):
+                    fn()
+        return graph_time(torch, stream, gr, max(1, args.steps // REP), REP)
+
+    res = {}
+    for name, wb in (("prefill", workloads.qwen25_3b_prefill()), ("decode", workloads.qwen25_3b_decode())):
+        print(f"bench: rope + append, {name} batch", file=sys.stderr, flush=True)
+        dv = wb.to(dev)
+        cos, sin = cos_sin(wb.positions, wb.d)
+        cd, sd = cos.to(dev), sin.to(dev)
+        q_out = torch.empty_like(dv.q)
+
+        def fused():
+            ops.append_paged_kv_cache_with_rope(dv.q, dv.k_new, dv.v_new, cd, sd, dv.batch_indices,
+                                                dv.positions, dv.cache, dv.indices, dv.indptr, dv.last,
+                                                q_out=q_out)
+
+        def unfused():
+            qe, ke = apply_rotary_pos_emb(dv.q.transpose(0, 1)[None], dv.k_new.transpose(0, 1)[None],
+                                          cd[None], sd[None])
+            ops.append_paged_kv_cache(ke[0].transpose(0, 1), dv.v_new, dv.batch_indices, dv.positions,
+                                      dv.cache, dv.indices, dv.indptr, dv.last)
+            return qe
+
+        if not args.no_check:  # both sequences leave identical bits
+            fused()
+            c1, q1 = dv.cache.clone(), q_out.clone()
+            q2 = unfused()[0].transpose(0, 1)
+            torch.cuda.synchronize()
+            if not (torch.equal(c1.view(torch.int16), dv.cache.view(torch.int16))
+                    and torch.equal(q1.view(torch.int16), q2.contiguous().view(torch.int16))):
+                raise SystemExit("rope + append: fused and unfused results differ")
+        tf, tu = timed(fused), timed(unfused)
+        nnz = dv.q.shape[0]
+        nbytes = nnz * rope_bytes(wb.hq, wb.hkv, wb.d, 2)
+        res[name] = dict(tokens=nnz, fused_us=round(tf * 1e6, 3), unfused_us=round(tu * 1e6, 3),
+                         bytes=nbytes, gbs=round(nbytes / tf / 1e9, 2))
+        del dv
+    # CPU baseline: the oracle (per-op rounded numpy rotation + scatter) on one 512-token chunk
+    sb = workloads.build_batch([512], [512], 16, 2, 128, torch.float16, seed=3, fill_old=False)
+    c, s = cos_sin(sb.positions, 128)
+    iv = lambda t: t.view(torch.int16).numpy()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        cb, sbits = iv(c)[:, None], iv(s)[:, None]
+        rope_ref.rotate(iv(sb.q).view(np.uint16), cb.view(np.uint16), sbits.view(np.uint16), "float16")
+        k_rot = rope_ref.rotate(iv(sb.k_new).view(np.uint16), cb.view(np.uint16), sbits.view(np.uint16), "float16")
+        kv_ref.append(iv(sb.cache), k_rot.view(np.int16), iv(sb.v_new), sb.batch_indices.numpy(),
+                      sb.positions.numpy(), sb.indices.numpy(), sb.indptr.numpy(), 16)
+        times.append(time.perf_counter() - t0)
+    cpu_gbs = 512 * rope_bytes(16, 2, 128, 2) / statistics.median(times) / 1e9
+    p = res["prefill"]
+    result = {
+        "metric": "fused rotary embedding + paged K/V append GB/s (% HBM peak), Qwen2.5-3B, 4096-token chunked prefill",
+        "value": p["gbs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1)*0.5 activations, the model's cos/sin at the tokens' positions)",
+        "config": {"workload": "append_paged_kv_cache_with_rope, 8 requests x 512-token chunks onto prefixes "
+                               "U[0, 8192], Hq 16, Hkv 2, D 128, page 16; and the B=64 decode step",
+                   "bytes_per_token": rope_bytes(16, 2, 128, 2)},
+        "prefill": p, "decode": res["decode"],
+        "speedup_vs_unfused": {k: round(v["unfused_us"] / v["fused_us"], 2) for k, v in res.items()},
+        "roofline": {"bound": "hbm", "achieved": p["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(p["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": "one 512-token chunk: oracle rotation of q and k, then the oracle append "
+                                   "(which also copies its 40-page pool), median of 3",
+                         "cpu_model": cpu_model()},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def step36(args, torch, workloads, dev):
     """The 36-layer decode step at Qwen2.5-3B attention shape, batch 128, on a shared
     2048-token prefix (workloads.SharedPrefixDecodeLoop): per step, the host bookkeeping and
@@ -504,14 +607,16 @@ def main():
                     help="waves take pages on demand (faster, not bitwise reproducible)")
     ap.add_argument("--workload", default="qwen25_3b_b64",
                     choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill", "qwen25_3b_step36",
-                             "qwen25_3b_sampling"],
+                             "qwen25_3b_sampling", "qwen25_3b_rope_append"],
                     help="qwen25_3b_b64: the headline decode + append step (default); llama31_8b_b128: "
                          "long-context decode at Llama-3.1-8B shape, B=128, ~4.4 GB of K/V in a 20 GB pool "
                          "(decode only, generated on the device); qwen25_3b_prefill: chunked prefill, 8 "
                          "requests x 512-token chunks onto prefixes U[0, 8192] (the matrix-core roofline); "
                          "qwen25_3b_step36: the 36-layer graph-captured decode step, B=128, on a shared "
                          "2048-token prefix with pages allocated and freed by the device pool; "
-                         "qwen25_3b_sampling: top-k/top-p sampling of 128 rows of the 151,936-token vocabulary")
+                         "qwen25_3b_sampling: top-k/top-p sampling of 128 rows of the 151,936-token vocabulary; "
+                         "qwen25_3b_rope_append: the model's rotary embedding fused with the append, "
+                         "4096-token prefill chunk and B=64 decode step, against the unfused sequence")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="for counter runs: N eager decode and append launches, then N plain "
                          "copies of the decode's byte count (the counters' calibration), then exit")
@@ -536,6 +641,8 @@ def main():
         return step36(args, torch, workloads, dev)
     if args.workload == "qwen25_3b_sampling":
         return sampling(args, torch, dev)
+    if args.workload == "qwen25_3b_rope_append":
+        return rope_append(args, torch, workloads, ops, dev)
     print("bench: building Qwen2.5-3B B=64 decode batch", file=sys.stderr, flush=True)
     wb = workloads.qwen25_3b_decode()
     NL = args.layers

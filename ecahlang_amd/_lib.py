@@ -29,6 +29,11 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _vp, _i64, _vp,
          _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     ),
+    "pkv_append_paged_kv_cache_rope": (
+        _i32,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+         _vp, _vp, _i32, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+    ),
     "pkv_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i64]),
     "pkv_decode_workspace_init": (_i32, [_vp, _i32, _vp]),
     "pkv_decode_uses_mfma": (_i32, [_i32, _i32, _i32, _i32, _i32]),

@@ -145,3 +145,70 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
         kv_indptr.numel() - 1,
         cv.num_kv_heads, cv.head_dim, cv.page_size, dtype_code(cv.dtype), err_ptr,
         stream_ptr(cv.device)), "append_paged_kv_cache")
+
+
+def append_paged_kv_cache_with_rope(q: torch.Tensor, append_key: torch.Tensor, append_value: torch.Tensor,
+                                    cos: torch.Tensor, sin: torch.Tensor, batch_indices: torch.Tensor,
+                                    positions: torch.Tensor, paged_kv_cache: CacheT,
+                                    kv_indices: torch.Tensor, kv_indptr: torch.Tensor,
+                                    kv_last_page_len: torch.Tensor, kv_layout: str = "NHD",
+                                    q_out: torch.Tensor | None = None,
+                                    err_count: torch.Tensor | None = None) -> torch.Tensor:
+    """The model's rotary embedding on the new tokens, then the append, in one launch.
+
+    Equivalent, bit for bit, to ``q, k = apply_rotary_pos_emb(q, k, cos, sin)`` as the model
+    runs it (transformers/models/qwen2/modeling_qwen2.py:210-211) followed by
+    ``append_paged_kv_cache(k, append_value, ...)`` (ecahlang/main.py:62-66).  ``q``,
+    ``append_key`` and ``append_value`` are ``[nnz, heads, head_dim]`` row views; ``cos`` /
+    ``sin`` are the tokens' ``[nnz, head_dim]`` position-embedding rows in the cache dtype.
+    The rotated queries go to ``q_out`` (default: a new tensor; pass ``q`` to rotate in
+    place) and are returned.  The rotated keys exist only in the cache.
+    """
+    cv = CacheView(paged_kv_cache, kv_layout)
+    for t, n in ((append_key, "append_key"), (append_value, "append_value")):
+        if t.dtype != cv.dtype:
+            raise ValueError(f"{n} dtype {t.dtype} differs from the cache dtype {cv.dtype}")
+        if t.shape[1:] != (cv.num_kv_heads, cv.head_dim):
+            raise ValueError(f"{n} must be [nnz, {cv.num_kv_heads}, {cv.head_dim}]")
+    nnz = append_key.shape[0]
+    if q.dtype != cv.dtype or q.dim() != 3 or q.shape[0] != nnz or q.shape[2] != cv.head_dim:
+        raise ValueError(f"q must be [{nnz}, Hq, {cv.head_dim}] in {cv.dtype}")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        if t.dtype != cv.dtype or t.dim() != 2 or t.shape != (nnz, cv.head_dim) or t.stride(1) != 1:
+            raise ValueError(f"{n} must be [{nnz}, {cv.head_dim}] in {cv.dtype} with a unit inner stride")
+    if cos.stride(0) != sin.stride(0):
+        raise ValueError("cos and sin must share a row stride")
+    if cv.head_dim % 8:
+        raise ValueError("head_dim must be a multiple of 8")
+    if append_value.shape[0] != nnz or batch_indices.numel() < nnz or positions.numel() < nnz:
+        raise ValueError("q, append_key, append_value, batch_indices and positions disagree on nnz")
+    if q_out is None:
+        q_out = torch.empty_like(q)
+    elif q_out.shape != q.shape or q_out.dtype != q.dtype:
+        raise ValueError("q_out must match q's shape and dtype")
+    _i32(batch_indices, "batch_indices")
+    _i32(positions, "positions")
+    _i32(kv_indices, "kv_indices")
+    _i32(kv_indptr, "kv_indptr")
+    qsn, qsh = _row_strides(q, "q")
+    osn, osh = _row_strides(q_out, "q_out")
+    ksn, ksh = _row_strides(append_key, "append_key")
+    vsn, vsh = _row_strides(append_value, "append_value")
+    for t, n in ((q, "q"), (q_out, "q_out"), (append_key, "append_key"), (append_value, "append_value"),
+                 (cos, "cos"), (sin, "sin"), (batch_indices, "batch_indices"), (positions, "positions")):
+        if t.device != cv.device:
+            raise ValueError(f"{n} is on {t.device}, the cache on {cv.device}")
+    err_ptr = 0
+    if err_count is not None:
+        err_ptr = _i32(err_count, "err_count").data_ptr()
+    if nnz == 0:
+        return q_out
+    check(lib().pkv_append_paged_kv_cache_rope(
+        q.data_ptr(), qsn, qsh, q_out.data_ptr(), osn, osh, q.shape[1],
+        append_key.data_ptr(), ksn, ksh, append_value.data_ptr(), vsn, vsh,
+        cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+        batch_indices.data_ptr(), positions.data_ptr(), nnz, cv.k_ptr, cv.v_ptr, cv.page_stride,
+        cv.num_pages, kv_indices.data_ptr(), kv_indices.numel(), kv_indptr.data_ptr(),
+        kv_indptr.numel() - 1, cv.num_kv_heads, cv.head_dim, cv.page_size, dtype_code(cv.dtype), err_ptr,
+        stream_ptr(cv.device)), "append_paged_kv_cache_with_rope")
+    return q_out

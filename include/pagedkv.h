@@ -66,6 +66,28 @@ int pkv_append_paged_kv_cache(const void* append_key, int64_t k_stride_n, int64_
                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                               int32_t dtype, int32_t* err_count, void* stream);
 
+/* The model's rotary embedding on the new tokens' q and k, then the append, in one launch:
+ * apply_rotary_pos_emb (transformers/models/qwen2/modeling_qwen2.py:210-211, run just before
+ * the attention hook) followed by the hook's append (ecahlang/main.py:62-66 ->
+ * pkv_append_paged_kv_cache).  q rows [nnz, num_qo_heads, head_dim] are rotated into q_out
+ * (q_out == q rotates in place); key rows are rotated and scattered like
+ * pkv_append_paged_kv_cache; value rows are scattered unchanged.  cos / sin are the tokens'
+ * rows [nnz, head_dim] of the model's position embeddings (row stride cs_stride_n), in the
+ * cache dtype.  Rotation: x*cos + rotate_half(x)*sin with rotate_half(x) = cat(-x2, x1),
+ * each product and the sum rounded to the dtype, so the outputs are bit-identical to the
+ * model's rotation followed by the plain append.  head_dim must be a multiple of 8.  Bad
+ * metadata is skipped and counted once per token in *err_count (may be NULL). */
+int pkv_append_paged_kv_cache_rope(const void* q, int64_t q_stride_n, int64_t q_stride_h, void* q_out,
+                                   int64_t qo_stride_n, int64_t qo_stride_h, int32_t num_qo_heads,
+                                   const void* append_key, int64_t k_stride_n, int64_t k_stride_h,
+                                   const void* append_value, int64_t v_stride_n, int64_t v_stride_h,
+                                   const void* cos, const void* sin, int64_t cs_stride_n,
+                                   const int32_t* batch_indices, const int32_t* positions, int32_t nnz,
+                                   void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
+                                   const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr,
+                                   int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                   int32_t dtype, int32_t* err_count, void* stream);
+
 /* Workspace bytes pkv_batch_decode needs for this geometry (num_indices = length of the
  * kv_indices buffer): the host half of BatchDecodeWithPagedKVCacheWrapper.plan
  * (ecahlang/main.py:341-347, :444-455).  The reference hands the wrapper a 128 MiB buffer
