@@ -93,7 +93,13 @@ __device__ __forceinline__ void st_dev4(float* base, uint32_t off, fvec4 v) {
   __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCpolSc1);
 }
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// vmcnt(0) through the builtin (expcnt and lgkmcnt left at their maxima: 0x0F70), so the
+// compiler's own wait bookkeeping knows every load and store has completed and inserts no
+// stale waits afterwards; the empty asm keeps memory accesses from moving across it.
+__device__ __forceinline__ void wait_stores() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
 
 // Workgroup barrier for LDS hand-offs only.  __syncthreads() also carries a release fence,
 // which on this target waits for every outstanding global load (vmcnt(0)) and so would
@@ -147,12 +153,14 @@ struct MergeItem {
     for (int s = 0; s < kMergeRegs; ++s) {
       const float c = (s < nseg && ml[s].y > 0.f) ? exp2f(ml[s].x - M) * ml[s].y : 0.f;
       den += c;
-      if (c != 0.f) {  // (a dropped segment's row may hold anything)
-        acc.x += c * po[s].x;
-        acc.y += c * po[s].y;
-        acc.z += c * po[s].z;
-        acc.w += c * po[s].w;
-      }
+      // Selects, not a branch: a dropped segment's row may hold anything (0 * NaN), and a
+      // value used only under a branch lets the compiler sink its load into that branch,
+      // where it is issued late and waited for at once.
+      const bool use = c != 0.f;
+      acc.x += use ? c * po[s].x : 0.f;
+      acc.y += use ? c * po[s].y : 0.f;
+      acc.z += use ? c * po[s].z : 0.f;
+      acc.w += use ? c * po[s].w : 0.f;
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
     T* orow = reinterpret_cast<T*>(P.out) + b * P.o_sn + h * P.o_sh + d;
@@ -177,14 +185,23 @@ __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*
   const int per = P.hq * (D / 4);
   const int nitems = nm * per;
   const int nt = blockDim.x;
-  for (int base = 0; base < nitems; base += 2 * nt) {
+  auto round = [&](int base) __attribute__((always_inline)) {
     const int i0 = base + threadIdx.x, i1 = i0 + nt;
     MergeItem<T, D> a, c;
     a.load(P, list, per, i0, nitems);
     c.load(P, list, per, i1, nitems);
+    asm volatile("" ::: "memory");  // both items' loads are issued before either fold
     a.finish(P);
     c.finish(P);
-  }
+  };
+  // The first round (all of it when nitems <= 2 * blockDim.x, the usual case) is peeled off
+  // the loop: inside a loop, registers that the previous round's loads filled can make the
+  // compiler wait for those loads before issuing the next ones.  With no items (nm == 0:
+  // this workgroup arrived last for none of its splits) nothing runs: an item's loads use
+  // list rows that only exist when nitems > 0.
+  if (nitems <= 0) return;
+  round(0);
+  for (int base = 2 * nt; base < nitems; base += 2 * nt) round(base);
   for (int i = 0; i < nm; ++i)
     if (list[i][2] - list[i][1] + 1 > kMergeRegs) merge_partials<T, D>(P, list[i][0], list[i][1], list[i][2]);
 }
