@@ -182,6 +182,29 @@ def sampling(args, torch, dev):
     t = graph_time(torch, stream, gr, max(1, args.steps // REP), REP)
     nbytes = B * V * 2 + B * 4
     gbs = nbytes / t / 1e9
+
+    def timed(fn):
+        with torch.cuda.stream(stream):
+            fn()
+            torch.cuda.synchronize()
+            g2 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g2, stream=stream):
+                for _ in range(REP):
+                    fn()
+        return graph_time(torch, stream, g2, max(1, args.steps // REP), REP)
+
+    # the reference's default request (top_k 0 -> whole vocabulary, top_p 1): plain multinomial
+    t_default = timed(lambda: sample(x, 0, 1.0))
+    # with the serving loop's scaling (main.py:483-487): repetition-penalty rows and temperature,
+    # fused into the sampler against the eager `logits / mask_penalty[rows] / temperature`
+    table = torch.ones(B, V, dtype=torch.float16, device=dev)
+    table[:, ::97] = 1.0 / 1.1
+    prow = torch.arange(B, dtype=torch.int32, device=dev)
+    temp = torch.full((B,), 0.7, dtype=torch.float32, device=dev)
+    t_fused = timed(lambda: sample(x, k, p, penalty=table, penalty_rows=prow, temperature=temp))
+    t_eager = timed(lambda: sample(x / table[prow.long()] / temp.reshape(-1, 1), k, p))
+    from ecahlang_amd.sampling import scale_logits
+    t_scale = timed(lambda: scale_logits(x, table, prow, temp))
     # CPU baseline: torch's sort-based top-k / top-p sampling on this host, 8 rows
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -207,6 +230,9 @@ def sampling(args, torch, dev):
         "config": {"workload": "top_k_top_p_sampling_from_logits, 128 x 151936 fp16 logits, top_k 50, top_p 0.9",
                    "rows": B, "vocab": V},
         "sampling_us": round(t * 1e6, 3), "bytes": nbytes,
+        "default_params_us": round(t_default * 1e6, 3),
+        "scaled_fused_us": round(t_fused * 1e6, 3), "scaled_eager_us": round(t_eager * 1e6, 3),
+        "scale_logits_us": round(t_scale * 1e6, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": {"value": round(8 * V * 2 / statistics.median(times) / 1e9, 3), "unit": "GB/s",

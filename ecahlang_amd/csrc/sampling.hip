@@ -307,7 +307,95 @@ int launch_sample(const T* logits, int64_t row_stride, int rows, int vocab, cons
   return (int)hipGetLastError();
 }
 
+// The serving loop's scaling before sampling (ecahlang/main.py:169-170, 483-487), in one pass:
+//   out[b][i] = float32(T(logits[b][i] / penalty[penalty_rows[b]][i])) / temperature[b]
+// (`logits / mask_penalty` in the logits' dtype T, then `/ temperature` with a float32
+// temperature, which promotes to float32).  Both divisions are IEEE divisions, as the tensor
+// ops do them; a penalty or temperature of 1 leaves the value unchanged (x / 1 == x).  One
+// thread per 8 logits; memory-bound.
+template <typename T, bool VEC>
+__global__ void scale_logits_kernel(const T* __restrict__ logits, int64_t row_stride, int vocab,
+                                    const T* __restrict__ penalty, int64_t penalty_stride, int penalty_slots,
+                                    const int32_t* __restrict__ penalty_rows, const float* __restrict__ temperature,
+                                    float* __restrict__ out, int64_t out_stride) {
+  constexpr int N = 8;  // logits per thread: 16 bytes of fp16 / bf16, two 16-byte vectors of fp32
+  const int b = blockIdx.y;
+  const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * N;
+  if (i0 >= vocab) return;
+  const T* x = logits + (int64_t)b * row_stride;
+  const int prow = penalty ? penalty_rows[b] : 0;
+  const T* pen = penalty ? penalty + (int64_t)prow * penalty_stride : nullptr;
+  const float t = temperature ? temperature[b] : 1.f;
+  float* o = out + (int64_t)b * out_stride;
+  if (penalty && (prow < 0 || prow >= penalty_slots)) {  // no such penalty row: the row reads as NaN
+    for (int k = 0; k < N && i0 + k < vocab; ++k) o[i0 + k] = __builtin_nanf("");
+    return;
+  }
+  auto scale = [&](T xv, T pv) __attribute__((always_inline)) -> float {
+    float y = to_f32(xv);
+    if (pen) {
+      const float d = to_f32(pv);
+      if (d != 1.f) y = to_f32(from_f32<T>(y / d));
+    }
+    if (t != 1.f) y = y / t;
+    return y;
+  };
+  if (VEC && i0 + N <= vocab) {
+    T xs[N], ps[N];
+    static_assert(N * sizeof(T) % 16 == 0, "whole 16-byte vectors");
+#pragma unroll
+    for (int v = 0; v < (int)(N * sizeof(T) / 16); ++v) {
+      const uint4 w = *reinterpret_cast<const uint4*>(x + i0 + v * (16 / sizeof(T)));
+      __builtin_memcpy(xs + v * (16 / sizeof(T)), &w, 16);
+      const uint4 pw = pen ? *reinterpret_cast<const uint4*>(pen + i0 + v * (16 / sizeof(T))) : make_uint4(0, 0, 0, 0);
+      __builtin_memcpy(ps + v * (16 / sizeof(T)), &pw, 16);
+    }
+    float ys[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) ys[k] = scale(xs[k], ps[k]);
+#pragma unroll
+    for (int v = 0; v < N / 4; ++v)
+      *reinterpret_cast<float4*>(o + i0 + 4 * v) = make_float4(ys[4 * v], ys[4 * v + 1], ys[4 * v + 2], ys[4 * v + 3]);
+  } else {
+    for (int k = 0; k < N && i0 + k < vocab; ++k) o[i0 + k] = scale(x[i0 + k], pen ? pen[i0 + k] : from_f32<T>(1.f));
+  }
+}
+
 }  // namespace
+
+extern "C" int pkv_scale_logits(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab, int32_t dtype,
+                                const void* penalty, int64_t penalty_stride, int32_t penalty_slots,
+                                const int32_t* penalty_rows, const float* temperature, float* out,
+                                int64_t out_stride, void* stream) {
+  if (rows < 0 || vocab <= 0 || row_stride < vocab || out_stride < vocab || !out) return kBadArg;
+  if (penalty && (!penalty_rows || penalty_stride < vocab || penalty_slots <= 0)) return kBadArg;
+  if (rows == 0) return kOk;
+  if (rows > 65535) return kBadArg;
+  const dim3 grid((unsigned)((vocab + 8 * 256 - 1) / (8 * 256)), (unsigned)rows);
+  hipStream_t s = (hipStream_t)stream;
+  const int es = dtype == kF32 ? 4 : 2;
+  // 16-byte vectors when every row start is 16-byte aligned (base pointers and row strides)
+  const bool vec = ((uintptr_t)logits % 16 == 0) && (row_stride * es % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
+                   (out_stride * 4 % 16 == 0) &&
+                   (!penalty || (((uintptr_t)penalty % 16 == 0) && (penalty_stride * es % 16 == 0)));
+#define PKV_SCALE(T)                                                                                          \
+  do {                                                                                                        \
+    if (vec)                                                                                                  \
+      hipLaunchKernelGGL((scale_logits_kernel<T, true>), grid, dim3(256), 0, s, (const T*)logits, row_stride, \
+                         vocab, (const T*)penalty, penalty_stride, penalty_slots, penalty_rows, temperature, out,  \
+                         out_stride);                                                                         \
+    else                                                                                                      \
+      hipLaunchKernelGGL((scale_logits_kernel<T, false>), grid, dim3(256), 0, s, (const T*)logits, row_stride, \
+                         vocab, (const T*)penalty, penalty_stride, penalty_slots, penalty_rows, temperature, out, \
+                         out_stride);                                                                         \
+  } while (0)
+  if (dtype == kF16) PKV_SCALE(_Float16);
+  else if (dtype == kBF16) PKV_SCALE(__hip_bfloat16);
+  else if (dtype == kF32) PKV_SCALE(float);
+  else return kBadDType;
+#undef PKV_SCALE
+  return (int)hipGetLastError();
+}
 
 extern "C" int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                                         int32_t dtype, const int32_t* top_k, int32_t top_k_all,

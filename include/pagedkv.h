@@ -202,6 +202,19 @@ int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, int32_t row
                              const float* top_p, float top_p_all, const float* uniform,
                              int32_t* out, void* stream);
 
+/* The serving loop's scaling of the logits before sampling (ecahlang/main.py:169-170, 483-487,
+ * 566-579: `logits / mask_penalty[slot_of_row]` in the logits' dtype, then `/ temperature` with
+ * a float32 temperature, which promotes to float32), in one pass instead of a gather and two
+ * divisions: out[b][i] = float32(dtype(logits[b][i] / penalty[penalty_rows[b] * penalty_stride
+ * + i])) / temperature[b], with IEEE divisions, so the values are bit-identical to those tensor
+ * ops.  penalty (the logits' dtype, penalty_slots rows) and temperature (float32, one per row)
+ * may each be NULL; a row whose penalty_rows entry is outside [0, penalty_slots) is written as
+ * NaN (the sampler then returns -1 for it).  out is float32, rows <= 65535. */
+int pkv_scale_logits(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab, int32_t dtype,
+                     const void* penalty, int64_t penalty_stride, int32_t penalty_slots,
+                     const int32_t* penalty_rows, const float* temperature, float* out, int64_t out_stride,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,3 +102,113 @@ def test_graph_captured_sampling_replays():
         for r in range(8):
             assert sr.kept_set(xs[r], 50, 0.9)[int(d[r])]
     assert len({tuple(d.tolist()) for d in draws}) > 1  # fresh uniforms on every replay
+
+
+def _scaled_reference(x, table, rows, temp):
+    """The serving loop's eager scaling (ecahlang/main.py:483-487): logits / mask_penalty rows
+    in the logits' dtype, then / temperature [n, 1] float32 (which promotes to float32)."""
+    y = x
+    if table is not None:
+        y = y / table[rows.long()]
+    if temp is not None:
+        y = y / temp.reshape(-1, 1)
+    return y
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("which", ["both", "penalty", "temperature"])
+def test_scaled_sampling_equals_sampling_the_scaled_logits(dtype, which):
+    """Fused penalty + temperature: the token is exactly the one the plain sampler draws from
+    the eagerly scaled logits, for the same uniforms (so every filter sees identical values)."""
+    rows, vocab, slots = 16, 32000, 40
+    g = torch.Generator().manual_seed(77)
+    x = (torch.randn(rows, vocab, generator=g) * 3).to(dtype).to(DEV)
+    table = torch.ones(slots, vocab, dtype=dtype)
+    # repetition penalties on some tokens of some slots (main.py:522, 597: divided in place)
+    for s in range(0, slots, 3):
+        idx = torch.randint(0, vocab, (200,), generator=g)
+        table[s, idx] = (1.0 / torch.empty(200).uniform_(1.05, 1.5, generator=g)).to(dtype)
+        table[s, idx[:20]] = torch.tensor(1.3, dtype=dtype)
+    table = table.to(DEV)
+    prow = torch.randperm(slots, generator=g)[:rows].to(torch.int32).to(DEV)
+    temp = torch.tensor([1.0, 0.7, 1.3, 0.05, 2.0, 1.0, 0.9, 1.1] * 2, dtype=torch.float32).to(DEV)
+    pen_arg = table if which in ("both", "penalty") else None
+    temp_arg = temp if which in ("both", "temperature") else None
+    ref_logits = _scaled_reference(x, pen_arg, prow, temp_arg)
+    ks = torch.tensor([0, 1, 5, 50, vocab, 20, 1000, 0] * 2, dtype=torch.int32).to(DEV)
+    ps = torch.tensor([1.0, 1.0, 0.9, 0.5, 0.8, 0.95, 1.0, 0.3] * 2, dtype=torch.float32).to(DEV)
+    for trial in range(4):
+        u = torch.rand(rows, generator=g).to(DEV)
+        got = sample(x, ks, ps, uniform=u, penalty=pen_arg, penalty_rows=prow if pen_arg is not None else None,
+                     temperature=temp_arg)
+        want = sample(ref_logits.contiguous(), ks, ps, uniform=u)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (dtype, which, trial, got.tolist(), want.tolist())
+    # and the draw is the oracle's for the scaled row
+    _check_rows(ref_logits.float().cpu(), ks.cpu(), ps.cpu(), u.cpu(), got.cpu())
+
+
+def test_scaled_sampling_neutral_scaling_is_plain_sampling():
+    """A penalty table of ones and temperature 1 change nothing (x / 1 == x)."""
+    rows, vocab = 8, 4099  # (odd vocab: the element path for the row tails)
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(rows, vocab, generator=g) * 2).half().to(DEV)
+    table = torch.ones(4, vocab, dtype=torch.float16, device=DEV)
+    prow = torch.tensor([0, 1, 2, 3, 0, 1, 2, 3], dtype=torch.int32, device=DEV)
+    u = torch.rand(rows, generator=g).to(DEV)
+    a = sample(x, 30, 0.9, uniform=u, penalty=table, penalty_rows=prow, temperature=1.0)
+    b = sample(x, 30, 0.9, uniform=u)
+    assert torch.equal(a, b)
+
+
+def test_scaled_sampling_argument_checks():
+    x = torch.randn(4, 100, device=DEV).half()
+    table = torch.ones(4, 100, dtype=torch.float16, device=DEV)
+    with pytest.raises(ValueError):
+        sample(x, 5, 0.9, penalty=table)  # no penalty_rows
+    with pytest.raises(ValueError):
+        sample(x, 5, 0.9, penalty=table.float(), penalty_rows=torch.zeros(4, dtype=torch.int32, device=DEV))
+    with pytest.raises(ValueError):
+        sample(x, 5, 0.9, temperature=torch.ones(3, device=DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_scale_logits_is_bitwise_the_eager_scaling(dtype):
+    """scale_logits against the serving loop's own tensor ops, value for value."""
+    from ecahlang_amd.sampling import scale_logits
+    rows, vocab, slots = 12, 50001, 20  # (odd vocab: a partial last group of 8)
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(rows, vocab, generator=g) * 4).to(dtype)
+    x[0, :5] = torch.tensor([0.0, -0.0, float("inf"), float("-inf"), 1e-7]).to(dtype)
+    x = x.to(DEV)
+    table = torch.ones(slots, vocab, dtype=dtype)
+    idx = torch.randint(0, vocab, (slots, 500), generator=g)
+    table.scatter_(1, idx, (1.0 / torch.empty(slots, 500).uniform_(1.01, 2.0, generator=g)).to(dtype))
+    table = table.to(DEV)
+    prow = torch.randint(0, slots, (rows,), generator=g).to(torch.int32).to(DEV)
+    temp = torch.tensor([1.0, 0.7, 1.3, 0.05, 2.0, 0.99999994, 1.9999999, 0.3, 1.0, 3.7, 0.1, 1.1],
+                        dtype=torch.float32).to(DEV)
+    for pen, t in ((table, temp), (table, None), (None, temp), (None, 0.8)):
+        got = scale_logits(x, pen, prow if pen is not None else None, t)
+        want = x
+        if pen is not None:
+            want = want / pen[prow.long()]
+        if t is not None:
+            tt = t if isinstance(t, torch.Tensor) else torch.full((rows,), t, dtype=torch.float32, device=DEV)
+            want = want / tt.reshape(-1, 1)
+        want = want.float()
+        torch.cuda.synchronize()
+        assert got.dtype == torch.float32
+        assert torch.equal(got.view(torch.int32), want.contiguous().view(torch.int32)), (dtype, pen is None, t)
+
+
+def test_scale_logits_bad_penalty_row_reads_as_nan():
+    from ecahlang_amd.sampling import scale_logits
+    x = torch.randn(3, 1000, device=DEV).half()
+    table = torch.ones(4, 1000, dtype=torch.float16, device=DEV)
+    rows = torch.tensor([0, 9, -1], dtype=torch.int32, device=DEV)
+    y = scale_logits(x, table, rows, 0.5)
+    assert torch.equal(y[0], x[0].float() / 0.5)
+    assert torch.isnan(y[1]).all() and torch.isnan(y[2]).all()
+    tok = sample(x, 0, 1.0, uniform=torch.full((3,), 0.5, device=DEV), penalty=table, penalty_rows=rows)
+    assert tok[1].item() == -1 and tok[2].item() == -1 and 0 <= tok[0].item() < 1000
