@@ -33,11 +33,13 @@ __device__ __forceinline__ uint32_t fkey(float f) {
   if (f != f) return 0u;
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
-// Mass of a logit in 32-bit fixed point: round(exp(x - max) * 2^32) capped at 2^32 - 1 (exp <= 1).
+// Mass of a logit in 32-bit fixed point: floor(exp(x - max) * 2^32), capped at 4294967040 (the
+// largest float below 2^32), so it converts with one 32-bit instruction (a float -> 64-bit
+// integer conversion is a sequence of ten; this runs for every logit on several passes).
 __device__ __forceinline__ uint64_t fmass(float x, float mx) {
   const float d = x - mx;
   if (!(d > -23.f)) return 0;  // (also NaN): exp(-23) * 2^32 < 0.5
-  return (uint64_t)fminf(__expf(d) * 4294967296.0f, 4294967295.0f);
+  return (uint64_t)(uint32_t)fminf(__expf(d) * 4294967296.0f, 4294967040.0f);
 }
 
 template <typename T>
