@@ -120,10 +120,10 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   static_assert(kPidCap <= 4 * NT, "four page ids per thread");
   const int tg = (int)(P.num_indices < INT_MAX ? P.num_indices : INT_MAX);
   int pv[4];
+  int gp0 = 0, glen = 1, ng = 0;
   {
-    int gp0 = 0, glen = 1;
     if (tg > 0) {
-      const int ng = decode_ranges(N0, tg);
+      ng = decode_ranges(N0, tg);
       if (w0 < ng) {
         const Ranges rg(ng, tg);
         gp0 = rg.start(w0);
@@ -171,6 +171,13 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
     s_bf = INT_MAX;
     s_bl = -1;
   }
+  if (tg > 0 && w0 < ng) {  // the first range's page ids, as the speculative read gave them
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // ids outside the pool are read as absent (-1)
+      const int t = threadIdx.x + r * NT;
+      if (t < glen) s_pid[t] = ((int64_t)pv[r] >= 0 && (int64_t)pv[r] < P.num_pages) ? pv[r] : -1;
+    }
+  }
   if (blockIdx.x == 0) zero_empty_sequences<T, D>(P);
   lds_barrier();
   auto rd = [&](const int* lds_arr, int i) __attribute__((always_inline)) -> int {  // uniform LDS read
@@ -198,6 +205,36 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   for (int r = 0; r < VCH; ++r) {
     const int c = lane + 64 * r;
     voff[r] = (uint32_t)((c / CPR) * rowstride + 8 * (c % CPR));
+  }
+
+  // A page id outside the pool is read as page 0; its tokens are masked (nv = 0).  Past the
+  // range's end the last page is loaded again (an L2 hit, never used): loads that are always
+  // issued keep the compiler's count of loads in flight exact, so that using one buffer
+  // never waits for the other.
+  auto load_page = [&](int pgid, uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH]) __attribute__((always_inline)) {
+    const int pg = pgid < 0 ? 0 : pgid;
+    const T* kb = kc + (int64_t)pg * P.page_stride + hoff;  // uniform base
+    const T* vb = vc + (int64_t)pg * P.page_stride + hoff;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      kr[s] = *reinterpret_cast<const uint4*>(kb + koff + 32 * s);
+#pragma unroll
+    for (int r = 0; r < VCH; ++r) vr[r] = *reinterpret_cast<const uint4*>(vb + voff[r]);
+  };
+
+  // Early start (fixed split): when the speculative read of the first range's page ids held
+  // (the page list is exactly indptr[B] long and starts at page 0, so the range holds no pages
+  // before its first sequence), every wave requests its first two pages now, ahead of the
+  // segment search and the q rows.
+  uint4 kA[KSTEPS], vA[VCH], kB[KSTEPS], vB[VCH];
+  const bool early = !P.dynamic && tg > 0 && total == tg && rd(s_indptr, 0) == 0 && w0 < N;
+  if (early) {
+    const int len0 = R.start(w0 + 1) - R.start(w0);
+    auto pid0 = [&](int i) __attribute__((always_inline)) -> int {
+      return __builtin_amdgcn_readfirstlane(s_pid[i < len0 ? i : len0 - 1]);
+    };
+    load_page(pid0(active ? j : len0), kA, vA);
+    load_page(pid0(active ? j + J : len0), kB, vB);
   }
 
   // Deferred arrivals (split segments recorded in s_split; the count is kept in a register
@@ -340,21 +377,6 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   auto pid_at = [&](int i) __attribute__((always_inline)) -> int {  // id of range page i (uniform)
     return __builtin_amdgcn_readfirstlane(s_pid[i < len ? i : len - 1]);
   };
-  // A page id outside the pool is read as page 0; its tokens are masked (nv = 0).  Past the
-  // range's end the last page is loaded again (an L2 hit, never used): loads that are always
-  // issued keep the compiler's count of loads in flight exact, so that using one buffer
-  // never waits for the other.
-  auto load_page = [&](int pgid, uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH]) __attribute__((always_inline)) {
-    const int pg = pgid < 0 ? 0 : pgid;
-    const T* kb = kc + (int64_t)pg * P.page_stride + hoff;  // uniform base
-    const T* vb = vc + (int64_t)pg * P.page_stride + hoff;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-      kr[s] = *reinterpret_cast<const uint4*>(kb + koff + 32 * s);
-#pragma unroll
-    for (int r = 0; r < VCH; ++r) vr[r] = *reinterpret_cast<const uint4*>(vb + voff[r]);
-  };
-
   // ---- the range's pages, one loop per wave; sequence (segment) boundaries are crossed
   // inside it.  Every wave ends each segment of the range once and in order, so the
   // combine barriers match up even though waves reach them at different pages.
@@ -568,14 +590,21 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   start_segment();
   // Ping-pong buffers A and B.  A wave's pages come in increasing order (ia < ib < next ia
   // ...), so the first one past the range ends the wave's loop.
-  uint4 kA[KSTEPS], vA[VCH], kB[KSTEPS], vB[VCH];
   int ia = len, ib = len;
-  if (active) {
-    ia = grab();
-    ib = grab();
+  if (early && w == w0) {  // (requested before the loop: pages j and j + J)
+    if (active) {
+      ia = j;
+      ib = j + J;
+      next_static = j + 2 * J;
+    }
+  } else {
+    if (active) {
+      ia = grab();
+      ib = grab();
+    }
+    load_page(pid_at(ia), kA, vA);
+    load_page(pid_at(ib), kB, vB);
   }
-  load_page(pid_at(ia), kA, vA);
-  load_page(pid_at(ib), kB, vB);
   if (q_one && (int)threadIdx.x < nqc) *reinterpret_cast<u32x4*>(s_qw + (int64_t)threadIdx.x * 8) = qc0;
   lds_barrier();  // the q rows are staged
   while (ia < len) {
