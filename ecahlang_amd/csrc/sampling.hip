@@ -289,23 +289,290 @@ __device__ __forceinline__ void sample_row(const RowT& row, SampleLds& L, int b,
   }
 }
 
+// Whether row b is sampled from its whole distribution (no top-k, no top-p filter).
+__device__ __forceinline__ bool whole_row(int b, int vocab, const int32_t* top_k, int32_t top_k_all,
+                                          const float* top_p, float top_p_all) {
+  const int k = top_k ? top_k[b] : top_k_all;
+  const float pp = top_p ? top_p[b] : top_p_all;
+  return (k <= 0 || k >= vocab) && !(pp < 1.f);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void sample_kernel(const T* logits, int64_t row_stride, int vocab,
                                                           const int32_t* top_k, int32_t top_k_all,
                                                           const float* top_p, float top_p_all,
-                                                          const float* uniform, int32_t* out) {
+                                                          const float* uniform, int32_t* out, int skip_whole) {
   __shared__ SampleLds L;
   const int b = blockIdx.x;
+  if (skip_whole && whole_row(b, vocab, top_k, top_k_all, top_p, top_p_all)) return;  // (the split kernels')
   const T* p = logits + (int64_t)b * row_stride;
   const Row<T> row{p, vocab, ((uintptr_t)p % 16) == 0};
   sample_row<T>(row, L, b, vocab, top_k, top_k_all, top_p, top_p_all, uniform, out);
 }
 
+// ---- Whole-distribution rows (the serving loop's default request: top_k 0, top_p 1) over many
+// workgroups per row.  One workgroup per row leaves half the chip idle and is bound by the
+// vector ALU of the CUs it has, so these rows are cut into slices of kSliceTiles tiles of
+// kSplitTile logits, one workgroup per (slice, row), in two launches:
+//   split_max_kernel     each slice's largest logit
+//   split_sample_kernel  the row's largest logit from the slices', each tile's mass (the same
+//                        integer masses as sample_row), then the workgroup that finishes its
+//                        slice last (a per-row counter) finds the tile and the token holding the
+//                        row's uniform, walking in vocabulary order.
+// The masses and the target are the integers sample_row computes, so the token is identical.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitTile = kSplitThreads * 8;  // 8 logits per thread
+constexpr int kSliceTiles = 8;
+constexpr int kMaxSplitTiles = 2048;           // vocabularies up to 4 M
+
+struct SplitWs {
+  uint64_t* tmass;   // [rows][ntiles] tile masses
+  float* smax;       // [rows][slices] slice maxima
+  int32_t* counter;  // [rows] arrivals at the end of split_sample_kernel
+};
+__host__ __device__ inline int split_tiles(int vocab) { return (vocab + kSplitTile - 1) / kSplitTile; }
+__host__ __device__ inline int split_slices(int vocab) { return (split_tiles(vocab) + kSliceTiles - 1) / kSliceTiles; }
+__host__ __device__ inline int64_t split_ws_bytes(int rows, int vocab) {
+  return (int64_t)rows * split_tiles(vocab) * 8 + (int64_t)rows * split_slices(vocab) * 4 + (int64_t)rows * 4;
+}
+__host__ __device__ inline SplitWs split_ws(void* ws, int rows, int vocab) {
+  char* c = reinterpret_cast<char*>(ws);
+  SplitWs w;
+  w.tmass = reinterpret_cast<uint64_t*>(c);
+  c += (int64_t)rows * split_tiles(vocab) * 8;
+  w.smax = reinterpret_cast<float*>(c);
+  c += (int64_t)rows * split_slices(vocab) * 4;
+  w.counter = reinterpret_cast<int32_t*>(c);
+  return w;
+}
+
+// Thread t's 8 logits of tile j: indices j * kSplitTile + 8 t .. + 7 (ok: inside the row).
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, int vocab, bool vec, int j, float (&x)[8], bool (&ok)[8]) {
+  const int base = j * kSplitTile + 8 * (int)threadIdx.x;
+  if (vec && base + 8 <= vocab) {
+    T e[8];
+#pragma unroll
+    for (int v = 0; v < (int)(8 * sizeof(T) / 16); ++v) {
+      const uint4 w = *reinterpret_cast<const uint4*>(p + base + v * (16 / sizeof(T)));
+      __builtin_memcpy(e + v * (16 / sizeof(T)), &w, 16);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x[k] = to_f32(e[k]);
+      ok[k] = true;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      ok[k] = base + k < vocab;
+      x[k] = ok[k] ? to_f32(p[base + k]) : 0.f;
+    }
+  }
+}
+
+// A slice's tiles for thread t, all loads issued before any is used: 16-byte vectors from
+// clamped in-bounds addresses (a load under a divergent branch would be waited for at the
+// branch's end, one tile at a time); get() then reads them, or the row with element loads
+// where a vector would cross its end (or the row is not 16-byte aligned).
+template <typename T>
+struct SliceLoad {
+  static constexpr int R = 8 * sizeof(T) / 16;  // vectors per thread per tile
+  uint4 raw[kSliceTiles][R];
+  __device__ __forceinline__ void issue(const T* p, int vocab, bool vec, int j0, int j1) {
+    if (!(vec && vocab >= 8)) return;  // (uniform)
+    const int last = (vocab - 8) / 8 * 8;
+#pragma unroll
+    for (int jj = 0; jj < kSliceTiles; ++jj) {
+      const int j = min(j0 + jj, j1 - 1);
+      const int base = min(j * kSplitTile + 8 * (int)threadIdx.x, last);
+#pragma unroll
+      for (int v = 0; v < R; ++v) raw[jj][v] = *reinterpret_cast<const uint4*>(p + base + v * (16 / sizeof(T)));
+    }
+  }
+  __device__ __forceinline__ void get(const T* p, int vocab, bool vec, int j, int jj, float (&x)[8],
+                                      bool (&ok)[8]) const {
+    const int base = j * kSplitTile + 8 * (int)threadIdx.x;
+    if (vec && vocab >= 8 && base + 8 <= vocab) {
+      T e[8];
+      __builtin_memcpy(e, raw[jj], 8 * sizeof(T));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        x[k] = to_f32(e[k]);
+        ok[k] = true;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        ok[k] = base + k < vocab;
+        x[k] = ok[k] ? to_f32(p[base + k]) : 0.f;
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ uint64_t block_sum256(uint64_t v, uint64_t* red) {
+  v = wave_sum_u64(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void split_max_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                  const int32_t* top_k, int32_t top_k_all,
+                                                                  const float* top_p, float top_p_all,
+                                                                  SplitWs ws) {
+  __shared__ float red[4];
+  const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
+  if (!whole_row(b, vocab, top_k, top_k_all, top_p, top_p_all)) return;
+  if (s == 0 && threadIdx.x == 0) ws.counter[b] = 0;  // (read by the next launch on this stream)
+  const T* p = logits + (int64_t)b * row_stride;
+  const bool vec = ((uintptr_t)p % 16) == 0;
+  float mx = -INFINITY;
+  const int j0 = s * kSliceTiles, j1 = min(j0 + kSliceTiles, ntiles);
+  SliceLoad<T> sl;
+  sl.issue(p, vocab, vec, j0, j1);
+#pragma unroll
+  for (int jj = 0; jj < kSliceTiles; ++jj) {
+    if (j0 + jj >= j1) break;  // (uniform)
+    float x[8];
+    bool ok[8];
+    sl.get(p, vocab, vec, j0 + jj, jj, x, ok);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (ok[k]) mx = fmaxf(mx, x[k]);
+  }
+  mx = block_max256(mx, red);
+  if (threadIdx.x == 0) ws.smax[(int64_t)b * S + s] = mx;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void split_sample_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                     const int32_t* top_k, int32_t top_k_all,
+                                                                     const float* top_p, float top_p_all,
+                                                                     const float* uniform, int32_t* out, SplitWs ws) {
+  __shared__ float redf[4];
+  __shared__ uint64_t redu[4];
+  __shared__ uint64_t s_tile[kMaxSplitTiles];
+  __shared__ int s_last;
+  const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
+  if (!whole_row(b, vocab, top_k, top_k_all, top_p, top_p_all)) return;
+  const T* p = logits + (int64_t)b * row_stride;
+  const bool vec = ((uintptr_t)p % 16) == 0;
+  // this slice's logits (requested first), and the row's largest logit from the slices'
+  // (written by the previous launch)
+  const int j0 = s * kSliceTiles, j1 = min(j0 + kSliceTiles, ntiles);
+  SliceLoad<T> sl;
+  sl.issue(p, vocab, vec, j0, j1);
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < S; i += kSplitThreads) mx = fmaxf(mx, ws.smax[(int64_t)b * S + i]);
+  mx = block_max256(mx, redf);
+  // this slice's tile masses, written through to device scope
+  uint64_t* tm = ws.tmass + (int64_t)b * ntiles;
+#pragma unroll
+  for (int jj = 0; jj < kSliceTiles; ++jj) {
+    if (j0 + jj >= j1) break;  // (uniform)
+    float x[8];
+    bool ok[8];
+    sl.get(p, vocab, vec, j0 + jj, jj, x, ok);
+    uint64_t m = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (ok[k]) m += fmass(x[k], mx);
+    m = block_sum256(m, redu);
+    if (threadIdx.x == 0) __hip_atomic_store(tm + j0 + jj, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // arrival: the last slice of the row to finish samples it
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // this slice's tile masses are complete (device-visible)
+    const int old = atomicAdd(&ws.counter[b], 1);
+    s_last = old == S - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (int j = threadIdx.x; j < ntiles; j += kSplitThreads)
+    s_tile[j] = __hip_atomic_load(tm + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  uint64_t ms = 0;
+  for (int j = 0; j < ntiles; ++j) ms += s_tile[j];  // (every thread: uniform)
+  if (ms == 0) {
+    if (threadIdx.x == 0) out[b] = -1;  // (no token carries mass: an all-NaN row)
+    return;
+  }
+  const double uu = fminf(fmaxf(uniform[b], 0.f), 1.f);
+  uint64_t target = (uint64_t)(uu * (double)ms);
+  if (target >= ms) target = ms - 1;
+  int tt = 0;
+  uint64_t before = 0;
+  while (tt < ntiles - 1 && before + s_tile[tt] <= target) before += s_tile[tt++];
+  // inside tile tt: each thread's mass, exclusive scan in thread (= vocabulary) order, then the
+  // owner walks its 8 logits
+  float x[8];
+  bool ok[8];
+  load8(p, vocab, vec, tt, x, ok);
+  uint64_t mine = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (ok[k]) mine += fmass(x[k], mx);
+  uint64_t inc = mine;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t v = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += v;
+  }
+  __syncthreads();
+  if (lane == 63) redu[wv] = inc;
+  __syncthreads();
+  uint64_t off = before;
+  for (int i = 0; i < wv; ++i) off += redu[i];
+  const uint64_t start = off + inc - mine;
+  if (mine > 0 && start <= target && target < start + mine) {
+    uint64_t run = start;
+    int found = -1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (found < 0 && ok[k]) {
+        run += fmass(x[k], mx);
+        if (run > target) found = tt * kSplitTile + 8 * (int)threadIdx.x + k;
+      }
+    }
+    out[b] = found;
+  }
+}
+
 template <typename T>
 int launch_sample(const T* logits, int64_t row_stride, int rows, int vocab, const int32_t* top_k, int32_t top_k_all,
-                  const float* top_p, float top_p_all, const float* uniform, int32_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(sample_kernel<T>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab, top_k,
-                     top_k_all, top_p, top_p_all, uniform, out);
+                  const float* top_p, float top_p_all, const float* uniform, int32_t* out, void* ws,
+                  int64_t ws_bytes, hipStream_t s) {
+  // which kernels have rows: scalars settle it on the host, per-row tensors need both
+  bool any_whole = true, any_other = true;
+  if (!top_k && !top_p) {
+    any_whole = (top_k_all <= 0 || top_k_all >= vocab) && !(top_p_all < 1.f);
+    any_other = !any_whole;
+  }
+  const bool split = ws && any_whole && rows <= 65535 && split_tiles(vocab) <= kMaxSplitTiles &&
+                     ws_bytes >= split_ws_bytes(rows, vocab);
+  if (split) {
+    const SplitWs w = split_ws(ws, rows, vocab);
+    const dim3 grid((unsigned)split_slices(vocab), (unsigned)rows);
+    hipLaunchKernelGGL(split_max_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
+                       top_k_all, top_p, top_p_all, w);
+    hipLaunchKernelGGL(split_sample_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
+                       top_k_all, top_p, top_p_all, uniform, out, w);
+  }
+  if (!split || any_other)
+    hipLaunchKernelGGL(sample_kernel<T>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab, top_k,
+                       top_k_all, top_p, top_p_all, uniform, out, split ? 1 : 0);
   return (int)hipGetLastError();
 }
 
@@ -399,10 +666,10 @@ extern "C" int pkv_scale_logits(const void* logits, int64_t row_stride, int32_t 
   return (int)hipGetLastError();
 }
 
-extern "C" int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
-                                        int32_t dtype, const int32_t* top_k, int32_t top_k_all,
-                                        const float* top_p, float top_p_all, const float* uniform,
-                                        int32_t* out, void* stream) {
+static int sample_entry(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab, int32_t dtype,
+                        const int32_t* top_k, int32_t top_k_all, const float* top_p, float top_p_all,
+                        const float* uniform, int32_t* out, void* workspace, int64_t workspace_bytes,
+                        void* stream) {
   if (rows < 0 || vocab <= 0 || row_stride < vocab || !uniform || !out) return kBadArg;
   if (rows == 0) return kOk;
   const int es = dtype == kF32 ? 4 : 2;
@@ -410,12 +677,33 @@ extern "C" int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, 
   hipStream_t s = (hipStream_t)stream;
   if (dtype == kF16)
     return launch_sample((const _Float16*)logits, row_stride, rows, vocab, top_k, top_k_all, top_p, top_p_all,
-                         uniform, out, s);
+                         uniform, out, workspace, workspace_bytes, s);
   if (dtype == kBF16)
     return launch_sample((const __hip_bfloat16*)logits, row_stride, rows, vocab, top_k, top_k_all, top_p,
-                         top_p_all, uniform, out, s);
+                         top_p_all, uniform, out, workspace, workspace_bytes, s);
   if (dtype == kF32)
     return launch_sample((const float*)logits, row_stride, rows, vocab, top_k, top_k_all, top_p, top_p_all,
-                         uniform, out, s);
+                         uniform, out, workspace, workspace_bytes, s);
   return kBadDType;
+}
+
+extern "C" int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                                        int32_t dtype, const int32_t* top_k, int32_t top_k_all,
+                                        const float* top_p, float top_p_all, const float* uniform,
+                                        int32_t* out, void* stream) {
+  return sample_entry(logits, row_stride, rows, vocab, dtype, top_k, top_k_all, top_p, top_p_all, uniform, out,
+                      nullptr, 0, stream);
+}
+
+extern "C" int64_t pkv_sampling_workspace_bytes(int32_t rows, int32_t vocab) {
+  return rows > 0 && vocab > 0 ? split_ws_bytes(rows, vocab) : 0;
+}
+
+extern "C" int pkv_top_k_top_p_sampling_ws(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                                           int32_t dtype, const int32_t* top_k, int32_t top_k_all,
+                                           const float* top_p, float top_p_all, const float* uniform,
+                                           int32_t* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (workspace && ((uintptr_t)workspace % 8)) return kBadAlign;
+  return sample_entry(logits, row_stride, rows, vocab, dtype, top_k, top_k_all, top_p, top_p_all, uniform, out,
+                      workspace, workspace_bytes, stream);
 }

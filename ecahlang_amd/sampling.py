@@ -73,11 +73,13 @@ def top_k_top_p_sampling_from_logits(logits: torch.Tensor, top_k, top_p, indices
     out = torch.empty(rows, dtype=torch.int32, device=dev)
     if penalty is not None or temperature is not None:
         logits = scale_logits(logits, penalty, penalty_rows, temperature)
-    check(lib().pkv_top_k_top_p_sampling(
+    ws_bytes = lib().pkv_sampling_workspace_bytes(rows, vocab)
+    ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
+    check(lib().pkv_top_k_top_p_sampling_ws(
         logits.data_ptr(), logits.stride(0), rows, vocab, dtype_code(logits.dtype),
         k_t.data_ptr() if k_t is not None else None, int(k_all),
         p_t.data_ptr() if p_t is not None else None, float(p_all),
-        uniform.data_ptr(), out.data_ptr(), stream_ptr(dev)), "top-k / top-p sampling")
+        uniform.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), stream_ptr(dev)), "top-k / top-p sampling")
     return out
 
 

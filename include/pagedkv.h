@@ -202,6 +202,19 @@ int pkv_top_k_top_p_sampling(const void* logits, int64_t row_stride, int32_t row
                              const float* top_p, float top_p_all, const float* uniform,
                              int32_t* out, void* stream);
 
+/* Workspace bytes pkv_top_k_top_p_sampling_ws can use for rows x vocab. */
+int64_t pkv_sampling_workspace_bytes(int32_t rows, int32_t vocab);
+
+/* pkv_top_k_top_p_sampling with a workspace (8-byte aligned, workspace_bytes >=
+ * pkv_sampling_workspace_bytes): rows sampled from their whole distribution (top_k <= 0 or
+ * >= vocab and top_p >= 1, the serving loop's default request) are then spread over many
+ * workgroups per row instead of one.  Same tokens, bit for bit; the workspace needs no
+ * initialisation (its counters are reset by the call itself). */
+int pkv_top_k_top_p_sampling_ws(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                                int32_t dtype, const int32_t* top_k, int32_t top_k_all, const float* top_p,
+                                float top_p_all, const float* uniform, int32_t* out, void* workspace,
+                                int64_t workspace_bytes, void* stream);
+
 /* The serving loop's scaling of the logits before sampling (ecahlang/main.py:169-170, 483-487,
  * 566-579: `logits / mask_penalty[slot_of_row]` in the logits' dtype, then `/ temperature` with
  * a float32 temperature, which promotes to float32), in one pass instead of a gather and two

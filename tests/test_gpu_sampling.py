@@ -212,3 +212,73 @@ def test_scale_logits_bad_penalty_row_reads_as_nan():
     assert torch.isnan(y[1]).all() and torch.isnan(y[2]).all()
     tok = sample(x, 0, 1.0, uniform=torch.full((3,), 0.5, device=DEV), penalty=table, penalty_rows=rows)
     assert tok[1].item() == -1 and tok[2].item() == -1 and 0 <= tok[0].item() < 1000
+
+
+def _single_wg(x, ks, ps, u):
+    """The one-workgroup-per-row kernel (the entry point without a workspace)."""
+    from ecahlang_amd._lib import dtype_code, lib, stream_ptr
+    rows, vocab = x.shape
+    out = torch.empty(rows, dtype=torch.int32, device=DEV)
+    k_t = ks if isinstance(ks, torch.Tensor) else None
+    p_t = ps if isinstance(ps, torch.Tensor) else None
+    rc = lib().pkv_top_k_top_p_sampling(
+        x.data_ptr(), x.stride(0), rows, vocab, dtype_code(x.dtype),
+        k_t.data_ptr() if k_t is not None else None, 0 if k_t is not None else int(ks),
+        p_t.data_ptr() if p_t is not None else None, 1.0 if p_t is not None else float(ps),
+        u.data_ptr(), out.data_ptr(), stream_ptr(DEV))
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("dtype,vocab", [(torch.float16, 151936), (torch.bfloat16, 32003), (torch.float32, 50000),
+                                         (torch.float16, 2048), (torch.float16, 7)])
+def test_whole_row_split_path_equals_single_workgroup(dtype, vocab):
+    """Rows sampled from their whole distribution run on many workgroups per row; the token
+    must be the one-workgroup kernel's, bit for bit, for the same uniforms."""
+    rows = 24
+    g = torch.Generator().manual_seed(vocab)
+    x = (torch.randn(rows, vocab, generator=g) * 3).to(dtype)
+    x[1] = float("nan")                     # no mass: -1
+    x[2, : vocab // 2] = float("nan")       # half NaN
+    x[3] = 0.0                              # uniform distribution
+    x[4, vocab // 3] = 50.0                 # one dominant logit
+    x = x.to(DEV)
+    u = torch.rand(rows, generator=g).to(DEV)
+    u[5], u[6] = 0.0, 0.9999999
+    want = _single_wg(x, 0, 1.0, u)
+    got = sample(x, 0, 1.0, uniform=u)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (got.tolist(), want.tolist())
+    assert got[1].item() == -1
+    assert got[4].item() == vocab // 3 or vocab < 3
+    # per-row parameters mixing whole rows with filtered ones: both paths in one call
+    ks = torch.tensor([0, vocab, 5, 0, 1, 0] * 4, dtype=torch.int32, device=DEV)
+    ps = torch.tensor([1.0, 1.0, 1.0, 0.7, 1.0, 1.5] * 4, dtype=torch.float32, device=DEV)
+    got2 = sample(x, ks, ps, uniform=u)
+    want2 = _single_wg(x, ks, ps, u)
+    torch.cuda.synchronize()
+    assert torch.equal(got2, want2)
+
+
+def test_whole_row_split_path_strided_rows_and_graph_replays():
+    vocab = 40001
+    base = (torch.randn(6, vocab + 5) * 2).half().to(DEV)
+    x = base[:, 3:3 + vocab]                 # rows not 16-byte aligned: element loads
+    u = torch.rand(6, device=DEV)
+    assert torch.equal(sample(x, 0, 1.0, uniform=u), _single_wg(x, 0, 1.0, u))
+    torch.manual_seed(11)
+    s = torch.cuda.Stream()
+    xc = base[:, :vocab].contiguous()
+    with torch.cuda.stream(s):
+        out = sample(xc, 0, 1.0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = sample(xc, 0, 1.0)
+    seen = []
+    for _ in range(5):
+        graph.replay()
+        torch.cuda.synchronize()
+        seen.append(out.cpu().clone())
+        assert ((seen[-1] >= 0) & (seen[-1] < vocab)).all()
+    assert len({tuple(t.tolist()) for t in seen}) > 1
