@@ -289,22 +289,30 @@ __device__ __forceinline__ void sample_row(const RowT& row, SampleLds& L, int b,
   }
 }
 
-// Whether row b is sampled from its whole distribution (no top-k, no top-p filter).
-__device__ __forceinline__ bool whole_row(int b, int vocab, const int32_t* top_k, int32_t top_k_all,
-                                          const float* top_p, float top_p_all) {
-  const int k = top_k ? top_k[b] : top_k_all;
-  const float pp = top_p ? top_p[b] : top_p_all;
-  return (k <= 0 || k >= vocab) && !(pp < 1.f);
+// Which kernel samples a row: its whole distribution (no top-k, no top-p filter), a top-k filter
+// with k <= kTopKMax (then any top-p), or anything else (the one-workgroup kernel).
+enum RowKind : int { kWholeRow = 0, kTopKRow = 1, kOtherRow = 2 };
+constexpr int kTopKMax = 256;
+__host__ __device__ __forceinline__ int row_kind_of(int k, float pp, int vocab) {
+  if (k <= 0 || k >= vocab) return pp < 1.f ? kOtherRow : kWholeRow;
+  return k <= kTopKMax ? kTopKRow : kOtherRow;
+}
+__device__ __forceinline__ int row_kind(int b, int vocab, const int32_t* top_k, int32_t top_k_all,
+                                        const float* top_p, float top_p_all) {
+  return row_kind_of(top_k ? top_k[b] : top_k_all, top_p ? top_p[b] : top_p_all, vocab);
 }
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void sample_kernel(const T* logits, int64_t row_stride, int vocab,
                                                           const int32_t* top_k, int32_t top_k_all,
                                                           const float* top_p, float top_p_all,
-                                                          const float* uniform, int32_t* out, int skip_whole) {
+                                                          const float* uniform, int32_t* out, int split,
+                                                          const int32_t* fallback) {
   __shared__ SampleLds L;
   const int b = blockIdx.x;
-  if (skip_whole && whole_row(b, vocab, top_k, top_k_all, top_p, top_p_all)) return;  // (the split kernels')
+  // with the split kernels in use, whole-distribution and small-top-k rows are theirs, except
+  // the rows they handed back (fallback[b])
+  if (split && row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kOtherRow && !fallback[b]) return;
   const T* p = logits + (int64_t)b * row_stride;
   const Row<T> row{p, vocab, ((uintptr_t)p % 16) == 0};
   sample_row<T>(row, L, b, vocab, top_k, top_k_all, top_p, top_p_all, uniform, out);
@@ -325,24 +333,38 @@ constexpr int kSplitTile = kSplitThreads * 8;  // 8 logits per thread
 constexpr int kSliceTiles = 8;
 constexpr int kMaxSplitTiles = 2048;           // vocabularies up to 4 M
 
+constexpr int kCandCap = 512;    // candidates a slice hands over for a top-k row
+constexpr int kMergeRegs = 16;   // candidates per lane of the merging wave (64 * 16 per row)
+
 struct SplitWs {
-  uint64_t* tmass;   // [rows][ntiles] tile masses
-  float* smax;       // [rows][slices] slice maxima
-  int32_t* counter;  // [rows] arrivals at the end of split_sample_kernel
+  uint64_t* tmass;    // [rows][ntiles] tile masses (whole rows)
+  uint64_t* cand;     // [rows][slices][kCandCap] candidates, index << 32 | key (top-k rows)
+  float* smax;        // [rows][slices] slice maxima (whole rows)
+  int32_t* ncand;     // [rows][slices] candidates per slice, -1: more than kCandCap
+  int32_t* counter;   // [rows] slices finished
+  int32_t* fallback;  // [rows] 1: handed back to the one-workgroup kernel
 };
 __host__ __device__ inline int split_tiles(int vocab) { return (vocab + kSplitTile - 1) / kSplitTile; }
 __host__ __device__ inline int split_slices(int vocab) { return (split_tiles(vocab) + kSliceTiles - 1) / kSliceTiles; }
 __host__ __device__ inline int64_t split_ws_bytes(int rows, int vocab) {
-  return (int64_t)rows * split_tiles(vocab) * 8 + (int64_t)rows * split_slices(vocab) * 4 + (int64_t)rows * 4;
+  const int64_t S = split_slices(vocab);
+  return (int64_t)rows * (split_tiles(vocab) * 8 + S * kCandCap * 8 + S * 4 + S * 4 + 4 + 4);
 }
 __host__ __device__ inline SplitWs split_ws(void* ws, int rows, int vocab) {
+  const int64_t S = split_slices(vocab);
   char* c = reinterpret_cast<char*>(ws);
   SplitWs w;
   w.tmass = reinterpret_cast<uint64_t*>(c);
   c += (int64_t)rows * split_tiles(vocab) * 8;
+  w.cand = reinterpret_cast<uint64_t*>(c);
+  c += (int64_t)rows * S * kCandCap * 8;
   w.smax = reinterpret_cast<float*>(c);
-  c += (int64_t)rows * split_slices(vocab) * 4;
+  c += (int64_t)rows * S * 4;
+  w.ncand = reinterpret_cast<int32_t*>(c);
+  c += (int64_t)rows * S * 4;
   w.counter = reinterpret_cast<int32_t*>(c);
+  c += (int64_t)rows * 4;
+  w.fallback = reinterpret_cast<int32_t*>(c);
   return w;
 }
 
@@ -433,8 +455,11 @@ __global__ __launch_bounds__(kSplitThreads) void split_max_kernel(const T* logit
                                                                   SplitWs ws) {
   __shared__ float red[4];
   const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
-  if (!whole_row(b, vocab, top_k, top_k_all, top_p, top_p_all)) return;
-  if (s == 0 && threadIdx.x == 0) ws.counter[b] = 0;  // (read by the next launch on this stream)
+  if (s == 0 && threadIdx.x == 0) {  // (read by the later launches on this stream)
+    ws.counter[b] = 0;
+    ws.fallback[b] = 0;
+  }
+  if (row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kWholeRow) return;
   const T* p = logits + (int64_t)b * row_stride;
   const bool vec = ((uintptr_t)p % 16) == 0;
   float mx = -INFINITY;
@@ -465,7 +490,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_sample_kernel(const T* lo
   __shared__ uint64_t s_tile[kMaxSplitTiles];
   __shared__ int s_last;
   const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
-  if (!whole_row(b, vocab, top_k, top_k_all, top_p, top_p_all)) return;
+  if (row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kWholeRow) return;
   const T* p = logits + (int64_t)b * row_stride;
   const bool vec = ((uintptr_t)p % 16) == 0;
   // this slice's logits (requested first), and the row's largest logit from the slices'
@@ -550,29 +575,299 @@ __global__ __launch_bounds__(kSplitThreads) void split_sample_kernel(const T* lo
   }
 }
 
+__device__ __forceinline__ int block_sum_i256(int v, int* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+__device__ __forceinline__ uint32_t block_max_u256(uint32_t v, uint32_t* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+// The float whose fkey is k (k != 0).
+__device__ __forceinline__ float key_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// ---- Top-k rows (0 < k <= kTopKMax, any top-p) over many workgroups per row, one launch.
+// Each (slice, row) workgroup holds its slice's keys in registers and bisects for a key t_s
+// with k <= #{key >= t_s} <= kCandCap (or takes every non-NaN logit when there are at most
+// kCandCap of them), and hands those logits over as candidates.  No slice can hold k logits
+// above the row's k-th largest key T*, so t_s <= T* and every logit with key >= T* is a
+// candidate: over the candidates, the largest T with #{key >= T} >= k is T* itself.  The last
+// slice of the row to finish then runs sample_row's rule on the candidates alone: T*, the top-p
+// threshold (the largest T with mass{key >= T} >= need, as its mass-weighted selection finds),
+// and the inverse CDF in vocabulary order, with the same integer masses, so the token is the
+// same.  One wave does that merge with shuffle reductions (a search takes up to 32 steps, and
+// workgroup barriers at every step made it the kernel's critical path); slices hand over between
+// k and 2k logits to keep the candidates within its registers.  Rows it cannot finish this way
+// (a slice's ties beyond kCandCap, more candidates than the wave holds, fewer than k finite
+// logits, a kept set beyond kKeptCap) are handed back to sample_kernel through `fallback`.
+constexpr int kKeptCap = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                   const int32_t* top_k, int32_t top_k_all,
+                                                                   const float* top_p, float top_p_all,
+                                                                   const float* uniform, int32_t* out, SplitWs ws) {
+  __shared__ int redi[4];
+  __shared__ uint32_t redk[4];
+  __shared__ uint64_t redu[4];
+  __shared__ int s_n, s_last, s_bad;
+  __shared__ int s_off[kMaxSplitTiles / kSliceTiles + 1];
+  __shared__ int s_sidx[kKeptCap];
+  __shared__ uint64_t s_smass[kKeptCap];
+  const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
+  if (row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kTopKRow) return;
+  const int k = top_k ? top_k[b] : top_k_all;
+  const T* p = logits + (int64_t)b * row_stride;
+  const bool vec = ((uintptr_t)p % 16) == 0;
+  if (threadIdx.x == 0) s_n = 0;
+  // the slice's keys (0: past the row's end, or NaN)
+  const int j0 = s * kSliceTiles, j1 = min(j0 + kSliceTiles, ntiles);
+  SliceLoad<T> sl;
+  sl.issue(p, vocab, vec, j0, j1);
+  uint32_t key[kSliceTiles * 8];
+#pragma unroll
+  for (int jj = 0; jj < kSliceTiles; ++jj) {
+    float x[8];
+    bool ok[8];
+    if (j0 + jj < j1) {
+      sl.get(p, vocab, vec, j0 + jj, jj, x, ok);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ok[e] = false;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) key[jj * 8 + e] = ok[e] ? fkey(x[e]) : 0u;
+  }
+  auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {  // #{key >= t}, t >= 1
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kSliceTiles * 8; ++i) c += key[i] >= t ? 1 : 0;
+    return block_sum_i256(c, redi);
+  };
+  uint32_t mk = 0;
+#pragma unroll
+  for (int i = 0; i < kSliceTiles * 8; ++i) mk = max(mk, key[i]);
+  mk = block_max_u256(mk, redk);
+  // hand over between k and 2k logits (fewer candidates keep the row's merge in one wave)
+  uint32_t ts = 1;
+  int cts = count_ge(1);
+  if (cts > 2 * k) {  // (uniform) bisect: count(lo) >= k > count(hi)
+    uint32_t lo = 1, hi = mk + 1u;
+    while (hi - lo > 1u) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      const int c = count_ge(mid);
+      if (c >= k) {
+        lo = mid;
+        cts = c;
+        if (c <= 2 * k) break;
+      } else {
+        hi = mid;
+      }
+    }
+    ts = lo;
+  }
+  const bool bad = cts > kCandCap;  // (ties at the threshold beyond the slice's capacity)
+  uint64_t* cand = ws.cand + ((int64_t)b * S + s) * kCandCap;
+  if (!bad) {
+#pragma unroll
+    for (int i = 0; i < kSliceTiles * 8; ++i) {
+      if (key[i] >= ts) {
+        const int pos = atomicAdd(&s_n, 1);
+        const int idx = (j0 + i / 8) * kSplitTile + 8 * (int)threadIdx.x + (i % 8);
+        __hip_atomic_store(cand + pos, ((uint64_t)(uint32_t)idx << 32) | key[i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // this thread's candidate stores are complete (device-visible)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(ws.ncand + (int64_t)b * S + s, bad ? -1 : s_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    const int old = atomicAdd(&ws.counter[b], 1);
+    s_last = old == S - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // ---- the row's last slice: the candidates of every slice
+  if (threadIdx.x == 0) {
+    int off = 0, anybad = 0;
+    for (int i = 0; i < S; ++i) {
+      const int c = __hip_atomic_load(ws.ncand + (int64_t)b * S + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_off[i] = off;
+      if (c < 0) anybad = 1;
+      off += c < 0 ? 0 : c;
+    }
+    s_off[S] = off;
+    s_bad = anybad || off == 0 || off > kWave * kMergeRegs;
+  }
+  __syncthreads();
+  const int n = s_off[S];
+  if (s_bad || n > kWave * kMergeRegs) {
+    if (threadIdx.x == 0) ws.fallback[b] = 1;
+    return;
+  }
+  // one wave merges (shuffle reductions, no workgroup barriers)
+  if (threadIdx.x >= kWave) return;
+  const int lane = threadIdx.x;
+  auto wsum_i = [](int v) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+  };
+  auto wmax_u = [](uint32_t v) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+    return v;
+  };
+  uint32_t ck[kMergeRegs];
+  int cidx[kMergeRegs];
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) {  // unconditional loads of clamped candidates
+    const int ci = min(lane + kWave * r, n - 1);
+    int lo = 0, hi = S;  // the slice holding candidate ci: s_off[lo] <= ci < s_off[lo + 1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_off[mid] <= ci) lo = mid; else hi = mid;
+    }
+    const uint64_t v = __hip_atomic_load(ws.cand + ((int64_t)b * S + lo) * kCandCap + (ci - s_off[lo]),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool real = lane + kWave * r < n;
+    ck[r] = real ? (uint32_t)v : 0u;
+    cidx[r] = (int)(v >> 32);
+  }
+  auto ccount = [&](uint32_t t) __attribute__((always_inline)) -> int {
+    int c = 0;
+#pragma unroll
+    for (int r = 0; r < kMergeRegs; ++r) c += ck[r] >= t ? 1 : 0;
+    return wsum_i(c);
+  };
+  uint32_t mxk = 0;
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) mxk = max(mxk, ck[r]);
+  mxk = wmax_u(mxk);
+  if (ccount(1) < k) {  // K would take NaN logits: not a candidate case
+    if (lane == 0) ws.fallback[b] = 1;
+    return;
+  }
+  // the k-th largest key T* (ties kept)
+  uint32_t thr;
+  {
+    uint32_t lo = 1, hi = mxk + 1u;
+    while (hi - lo > 1u) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      if (ccount(mid) >= k) lo = mid; else hi = mid;
+    }
+    thr = lo;
+  }
+  const float mx = key_float(mxk);
+  uint64_t cm[kMergeRegs];  // candidate masses (0 below T*)
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) cm[r] = ck[r] >= thr ? fmass(key_float(ck[r]), mx) : 0;
+  auto cmass = [&](uint32_t t) __attribute__((always_inline)) -> uint64_t {  // mass{key >= t}, t >= T*
+    uint64_t m = 0;
+#pragma unroll
+    for (int r = 0; r < kMergeRegs; ++r) m += ck[r] >= t ? cm[r] : 0;
+    return wave_sum_u64(m);
+  };
+  const float pp = top_p ? top_p[b] : top_p_all;
+  if (pp < 1.f) {
+    const uint64_t mkk = cmass(thr);
+    const double needd = ceil((double)fmaxf(pp, 0.f) * (double)mkk);
+    uint64_t need = needd < 1.0 ? 1 : (uint64_t)needd;
+    if (need > mkk) need = mkk;
+    if (mkk > 0) {  // the largest T with mass{key >= T} >= need
+      uint32_t lo = thr, hi = mxk + 1u;
+      while (hi - lo > 1u) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (cmass(mid) >= need) lo = mid; else hi = mid;
+      }
+      thr = lo;
+    }
+  }
+  // the kept set, compacted into LDS in a fixed order (ballots), then the inverse CDF in
+  // vocabulary order
+  uint64_t ms = 0;
+  int m = 0;
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) {
+    const bool keep = ck[r] >= thr;
+    const uint64_t bal = __ballot(keep);
+    if (keep) {
+      const int pos = m + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+      if (pos < kKeptCap) {
+        s_sidx[pos] = cidx[r];
+        s_smass[pos] = cm[r];
+      }
+      ms += cm[r];
+    }
+    m += __popcll(bal);
+  }
+  ms = wave_sum_u64(ms);
+  if (m > kKeptCap) {
+    if (lane == 0) ws.fallback[b] = 1;
+    return;
+  }
+  if (ms == 0) {
+    if (lane == 0) out[b] = -1;
+    return;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the kept set is in LDS for every lane
+  __builtin_amdgcn_wave_barrier();
+  const double uu = fminf(fmaxf(uniform[b], 0.f), 1.f);
+  uint64_t target = (uint64_t)(uu * (double)ms);
+  if (target >= ms) target = ms - 1;
+  for (int e = lane; e < m; e += kWave) {
+    const int ie = s_sidx[e];
+    uint64_t pre = 0;  // mass of the kept logits before this one in vocabulary order
+    for (int f = 0; f < m; ++f) pre += s_sidx[f] < ie ? s_smass[f] : 0;
+    if (s_smass[e] > 0 && pre <= target && target < pre + s_smass[e]) out[b] = ie;
+  }
+}
+
 template <typename T>
 int launch_sample(const T* logits, int64_t row_stride, int rows, int vocab, const int32_t* top_k, int32_t top_k_all,
                   const float* top_p, float top_p_all, const float* uniform, int32_t* out, void* ws,
                   int64_t ws_bytes, hipStream_t s) {
-  // which kernels have rows: scalars settle it on the host, per-row tensors need both
-  bool any_whole = true, any_other = true;
+  // which kinds of rows there are: scalars settle it on the host, per-row tensors need all
+  bool any_whole = true, any_topk = true, any_other = true;
   if (!top_k && !top_p) {
-    any_whole = (top_k_all <= 0 || top_k_all >= vocab) && !(top_p_all < 1.f);
-    any_other = !any_whole;
+    const int kind = row_kind_of(top_k_all, top_p_all, vocab);
+    any_whole = kind == kWholeRow;
+    any_topk = kind == kTopKRow;
+    any_other = kind == kOtherRow;
   }
-  const bool split = ws && any_whole && rows <= 65535 && split_tiles(vocab) <= kMaxSplitTiles &&
+  const bool split = ws && (any_whole || any_topk) && rows <= 65535 && split_tiles(vocab) <= kMaxSplitTiles &&
                      ws_bytes >= split_ws_bytes(rows, vocab);
+  SplitWs w{};
   if (split) {
-    const SplitWs w = split_ws(ws, rows, vocab);
+    w = split_ws(ws, rows, vocab);
     const dim3 grid((unsigned)split_slices(vocab), (unsigned)rows);
+    // (split_max_kernel also resets every row's counter and fallback flag for the kernels below)
     hipLaunchKernelGGL(split_max_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
                        top_k_all, top_p, top_p_all, w);
-    hipLaunchKernelGGL(split_sample_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
-                       top_k_all, top_p, top_p_all, uniform, out, w);
+    if (any_whole)
+      hipLaunchKernelGGL(split_sample_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
+                         top_k_all, top_p, top_p_all, uniform, out, w);
+    if (any_topk)
+      hipLaunchKernelGGL(split_topk_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
+                         top_k_all, top_p, top_p_all, uniform, out, w);
   }
-  if (!split || any_other)
+  if (!split || any_other || any_topk)  // (top-k rows may be handed back)
     hipLaunchKernelGGL(sample_kernel<T>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab, top_k,
-                       top_k_all, top_p, top_p_all, uniform, out, split ? 1 : 0);
+                       top_k_all, top_p, top_p_all, uniform, out, split ? 1 : 0, w.fallback);
   return (int)hipGetLastError();
 }
 

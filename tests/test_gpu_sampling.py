@@ -282,3 +282,59 @@ def test_whole_row_split_path_strided_rows_and_graph_replays():
         seen.append(out.cpu().clone())
         assert ((seen[-1] >= 0) & (seen[-1] < vocab)).all()
     assert len({tuple(t.tolist()) for t in seen}) > 1
+
+
+@pytest.mark.parametrize("dtype,vocab", [(torch.float16, 151936), (torch.bfloat16, 32003), (torch.float32, 20000),
+                                         (torch.float16, 300)])
+def test_top_k_split_path_equals_single_workgroup(dtype, vocab):
+    """Top-k rows (k <= 256, any top-p) run on many workgroups per row through per-slice
+    candidates; the token must be the one-workgroup kernel's, bit for bit, including rows the
+    split path hands back (ties beyond a slice's capacity, fewer than k finite logits)."""
+    rows = 32
+    g = torch.Generator().manual_seed(vocab + 1)
+    x = (torch.randn(rows, vocab, generator=g) * 3).to(dtype)
+    x[1] = torch.round(x[1])                          # heavy ties at every threshold
+    x[2] = 0.5                                        # one value everywhere: handed back
+    x[3, : vocab - 10] = float("nan")                 # fewer than k finite logits: handed back
+    x[4, 7] = 40.0                                    # one dominant logit
+    x[5, : vocab // 2] = float("-inf")
+    x[6] = x[6].sort(descending=True).values           # the top-k all in the first slice
+    x = x.to(DEV)
+    ks = torch.tensor([50, 1, 20, 5, 256, 3, 200, 2] * 4, dtype=torch.int32, device=DEV)
+    ps = torch.tensor([0.9, 1.0, 0.5, 1.0, 0.95, 0.3, 1.0, 0.99] * 4, dtype=torch.float32, device=DEV)
+    ks = torch.minimum(ks, torch.tensor(vocab - 1, dtype=torch.int32, device=DEV))
+    for trial in range(3):
+        u = torch.rand(rows, generator=g).to(DEV)
+        got = sample(x, ks, ps, uniform=u)
+        want = _single_wg(x, ks, ps, u)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (trial, (got != want).nonzero().flatten().tolist())
+    # scalar parameters (only the top-k kernels launched), and k = 257 (the one-workgroup kernel)
+    for kk, pp in ((50, 0.9), (1, 1.0), (256, 0.5), (257, 0.9)):
+        u = torch.rand(rows, generator=g).to(DEV)
+        got = sample(x, min(kk, vocab - 1), pp, uniform=u)
+        want = _single_wg(x, min(kk, vocab - 1), pp, u)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (kk, pp)
+
+
+def test_top_k_split_path_graph_replays():
+    x = (torch.randn(16, 151936, device=DEV) * 3).half()
+    torch.manual_seed(3)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        out = sample(x, 50, 0.9)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = sample(x, 50, 0.9)
+    xs = x.float().cpu().numpy()
+    seen = []
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        d = out.cpu().clone()
+        seen.append(tuple(d.tolist()))
+        for r in range(16):
+            assert sr.kept_set(xs[r], 50, 0.9)[int(d[r])]
+    assert len(set(seen)) > 1
