@@ -40,6 +40,7 @@ from __future__ import annotations
 import math
 from typing import Iterable
 
+import numpy as np
 import torch
 
 from ._lib import check, lib, stream_ptr
@@ -53,11 +54,49 @@ def get_total_free_memory(index: int = 0) -> int:
     return torch.cuda.mem_get_info(index)[0]
 
 
-def _to_device(values: list, device: torch.device) -> torch.Tensor:
-    """int32 values to the device through a pinned buffer, asynchronously on the current
-    stream (the caching host allocator keeps the buffer until the copy has run)."""
-    host = torch.tensor(values, dtype=torch.int32).pin_memory()
-    return host.to(device, non_blocking=True)
+class _Staging:
+    """Host -> device copies of int32 arrays through a ring of reused pinned buffers, queued on
+    the current stream.  ``host(n)`` hands out the next buffer once the event recorded behind
+    its last copy has completed (so a queued copy never sees its source change); ``send`` queues
+    the copy and records the buffer's event.  Arrays beyond the ring's capacity, and copies made
+    while the stream is being captured, go through a fresh pinned buffer instead, which the
+    caching host allocator keeps until its copy has run."""
+
+    def __init__(self, device: torch.device, slots: int = 8, cap: int = 1 << 15):
+        self.device, self.cap = device, cap
+        self.bufs = [torch.empty(cap, dtype=torch.int32, pin_memory=True) for _ in range(slots)]
+        self.views = [b.numpy() for b in self.bufs]
+        self.events = [torch.cuda.Event() for _ in range(slots)]
+        self.used = [False] * slots
+        self.i = 0
+
+    def host(self, n: int) -> tuple:
+        """(slot, int32 array of n to fill); slot -1 means the array is not a ring buffer."""
+        if n > self.cap or torch.cuda.is_current_stream_capturing():
+            return -1, np.empty(n, dtype=np.int32)
+        i = self.i
+        self.i = (i + 1) % len(self.bufs)
+        if self.used[i]:
+            self.events[i].synchronize()
+        return i, self.views[i][:n]
+
+    def send(self, slot: int, arr: np.ndarray, dst: torch.Tensor | None = None) -> torch.Tensor:
+        """Queue ``arr`` (from ``host``) into ``dst[:len(arr)]``, a new device tensor when
+        ``dst`` is None."""
+        n = len(arr)
+        src = self.bufs[slot][:n] if slot >= 0 else torch.from_numpy(arr).pin_memory()
+        if dst is None:
+            dst = torch.empty(n, dtype=torch.int32, device=self.device)
+        dst[:n].copy_(src, non_blocking=True)
+        if slot >= 0:
+            self.events[slot].record(torch.cuda.current_stream(self.device))
+            self.used[slot] = True
+        return dst
+
+    def copy(self, values: list, dst: torch.Tensor | None = None) -> torch.Tensor:
+        slot, arr = self.host(len(values))
+        arr[:] = values
+        return self.send(slot, arr, dst)
 
 
 class _FreeBlocks:
@@ -165,6 +204,7 @@ class AutoKVCacheManager:
         self._stride = max(1, min(max(self.max_blocks, 1), max_pages_per_seq))
         self._table = torch.full((self._rows, self._stride), -1, dtype=torch.int32, device=self.device)
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._staging = _Staging(self.device)
         self._ops: list = []
         self._n_padding = 0
         self._shared: dict = {}  # batch_id -> (prefix id, leading shared pages)
@@ -186,6 +226,7 @@ class AutoKVCacheManager:
         self._cg_batch_indices: dict = {}
         self._cg_positions: dict = {}
         self._cg_append_indptr: dict = {}
+        self._cg_meta: dict = {}  # bucket -> [desc | indptr | last_page_len | positions] (the three are views)
         # The pool's initial state (free stack, page table, cache) is written on the current
         # stream; a caller may go on to drive the pool from another stream, so it is complete
         # before the constructor returns.
@@ -206,26 +247,58 @@ class AutoKVCacheManager:
         if not self._ops:
             return
         flat = [x for op in self._ops for x in op]
-        ops = _to_device(flat, self.device)
+        ops = self._staging.copy(flat)
         check(lib().pkv_pool_apply(self._stack.data_ptr(), self.max_blocks, self._table.data_ptr(),
                                    self._stride, self._rows, ops.data_ptr(), len(self._ops),
                                    self._err.data_ptr(), stream_ptr(self.device)), "page pool update")
         self._ops = []
 
-    def _gather(self, desc: list, counts: list, out_indices: torch.Tensor, extra: list) -> torch.Tensor:
-        """indptr = exclusive scan of counts; out_indices[indptr[b] + k] = table[desc...].
-        Returns the device copy of [indptr | extra] (one asynchronous H2D copy)."""
+    def _stage_tables(self, ids: list, bucket: int = 0, positions: bool = False) -> tuple:
+        """The gather's input for the sequences ``ids`` followed by ``bucket - len(ids)``
+        padding rows (one padding page each, last_page_len 1, position 0), staged in one host
+        array: [desc (4 per row) | kv_indptr (rows + 1) | kv_last_page_len (rows)] plus
+        [positions (rows)] (each row's newest token) when asked.  Returns (slot, array, rows,
+        pages)."""
+        r = len(ids)
+        b = max(bucket, r)
+        if b - r > self._n_padding:
+            raise IndexError("list index out of range")
+        slots = np.fromiter(map(self.batch_to_seq_len.__getitem__, ids), np.int32, r)
+        npages = np.fromiter(map(self._npages.__getitem__, ids), np.int32, r)
+        plen = np.fromiter(map(self.batch_to_page_lengths.__getitem__, ids), np.int32, r)
+        slot, out = self._staging.host((7 if positions else 6) * b + 1)
+        desc = out[: 4 * b].reshape(b, 4)
+        desc[:r, 0] = slots
+        desc[r:, 0] = self._rows - 1
+        desc[:r, 1] = 0
+        desc[r:, 1] = np.arange(b - r, dtype=np.int32)
+        desc[:r, 2] = npages
+        desc[r:, 2] = 1
+        desc[:, 3] = 0
+        indptr = out[4 * b: 5 * b + 1]
+        indptr[0] = 0
+        np.cumsum(desc[:, 2], out=indptr[1:])
+        last = out[5 * b + 1: 6 * b + 1]
+        last[:r] = plen
+        last[r:] = 1
+        if positions:
+            pos = out[6 * b + 1: 7 * b + 1]
+            np.multiply(npages - 1, self.block_size, out=pos[:r])
+            pos[:r] += plen - 1
+            pos[r:] = 0
+        return slot, out, b, int(indptr[-1])
+
+    def _gather(self, slot: int, staged: np.ndarray, b: int, pages: int, out_indices: torch.Tensor,
+                dst: torch.Tensor | None = None) -> torch.Tensor:
+        """Copy the staged [desc | indptr | extra] to the device (into ``dst`` when given) and
+        gather out_indices[indptr[r] + k] = table[desc...]; returns the device [indptr | extra]."""
         self._flush()
-        b = len(counts)
-        indptr = [0]
-        for c in counts:
-            indptr.append(indptr[-1] + c)
-        dev = _to_device(desc + indptr + extra, self.device)
+        dev = self._staging.send(slot, staged, dst)
         d_desc, d_rest = dev[: 4 * b], dev[4 * b:]
-        if indptr[-1]:
+        if pages:
             check(lib().pkv_pool_gather(self._table.data_ptr(), self._stride, self._rows, d_desc.data_ptr(),
                                         d_rest.data_ptr(), b, out_indices.data_ptr(), out_indices.numel(),
-                                        indptr[-1], self._err.data_ptr(), stream_ptr(self.device)),
+                                        pages, self._err.data_ptr(), stream_ptr(self.device)),
                   "page table gather")
         return d_rest
 
@@ -338,15 +411,10 @@ class AutoKVCacheManager:
     def get_append_metadata(self, batch_ids: Iterable) -> tuple:
         """manager.py:122-138: (kv_indices, kv_indptr, kv_last_page_len), int32 on the device."""
         batch_ids = list(batch_ids)
-        desc, counts, last = [], [], []
-        for bid in batch_ids:
-            n = self._npages[bid]
-            desc += [self.batch_to_seq_len[bid], 0, n, 0]
-            counts.append(n)
-            last.append(self.batch_to_page_lengths[bid])
-        kv_indices = torch.empty(sum(counts), dtype=torch.int32, device=self.device)
-        rest = self._gather(desc, counts, kv_indices, last)
-        b = len(batch_ids)
+        self._flush()  # (the staging ring hands out buffers in order)
+        slot, staged, b, pages = self._stage_tables(batch_ids)
+        kv_indices = torch.empty(pages, dtype=torch.int32, device=self.device)
+        rest = self._gather(slot, staged, b, pages, kv_indices)
         return kv_indices, rest[: b + 1], rest[b + 1: 2 * b + 1]
 
     def prepare_append_metadata(self, batch_ids, append_indptr: torch.Tensor, nnz=None) -> None:
@@ -402,10 +470,14 @@ class AutoKVCacheManager:
         for bs in bucket_sizes:
             self._cg_kv_indices[bs] = torch.zeros(max(self.max_blocks, max_indices or 0), dtype=torch.int32,
                                                   device=dev)
-            self._cg_kv_indptr[bs] = torch.zeros(bs + 1, dtype=torch.int32, device=dev)
-            self._cg_kv_last_page_len[bs] = torch.zeros(bs, dtype=torch.int32, device=dev)
+            # indptr, last_page_len and positions are views of one block laid out as the
+            # metadata build stages them, so one host copy fills all three
+            meta = torch.zeros(7 * bs + 1, dtype=torch.int32, device=dev)
+            self._cg_meta[bs] = meta
+            self._cg_kv_indptr[bs] = meta[4 * bs: 5 * bs + 1]
+            self._cg_kv_last_page_len[bs] = meta[5 * bs + 1: 6 * bs + 1]
             self._cg_batch_indices[bs] = torch.arange(bs, dtype=torch.int32, device=dev)
-            self._cg_positions[bs] = torch.zeros(bs, dtype=torch.int32, device=dev)
+            self._cg_positions[bs] = meta[6 * bs + 1: 7 * bs + 1]
             self._cg_append_indptr[bs] = torch.arange(bs + 1, dtype=torch.int32, device=dev)
             self._cg_temperature[bs] = torch.ones(bs, 1, dtype=torch.float32, device=dev)
             self._cg_top_k[bs] = torch.full((bs,), self.vocab_size, dtype=torch.int32, device=dev)
@@ -416,28 +488,13 @@ class AutoKVCacheManager:
         newest token, then ``bucket - n`` padding rows (one padding page, last_page_len 1,
         position 0), written into the bucket's static buffers on the device."""
         real_uuids = list(real_uuids)
-        desc, counts, last, positions = [], [], [], []
-        for uid in real_uuids:
-            n = self._npages[uid]
-            pl = self.batch_to_page_lengths[uid]
-            desc += [self.batch_to_seq_len[uid], 0, n, 0]
-            counts.append(n)
-            last.append(pl)
-            positions.append((n - 1) * self.block_size + pl - 1)
-        for i in range(bucket_size - len(real_uuids)):
-            if i >= self._n_padding:
-                raise IndexError("list index out of range")
-            desc += [self._rows - 1, i, 1, 0]
-            counts.append(1)
-            last.append(1)
-            positions.append(0)
-        if sum(counts) > self._cg_kv_indices[bucket_size].numel():
+        self._flush()
+        slot, staged, b, pages = self._stage_tables(real_uuids, bucket_size, positions=True)
+        if pages > self._cg_kv_indices[bucket_size].numel():
             raise RuntimeError("page table larger than the bucket's kv_indices buffer")
-        rest = self._gather(desc, counts, self._cg_kv_indices[bucket_size], last + positions)
-        b = len(counts)
-        self._cg_kv_indptr[bucket_size].copy_(rest[: b + 1])
-        self._cg_kv_last_page_len[bucket_size].copy_(rest[b + 1: 2 * b + 1])
-        self._cg_positions[bucket_size].copy_(rest[2 * b + 1: 3 * b + 1])
+        # [desc | indptr | last | positions] lands in the bucket's block: the three buffers the
+        # captured step reads are views of it
+        self._gather(slot, staged, b, pages, self._cg_kv_indices[bucket_size], dst=self._cg_meta[bucket_size])
 
     def append_paged_kv_cache_cuda_graph(self, key, value, bucket_size: int, layer_idx: int) -> None:
         """manager.py:270-280."""
