@@ -111,35 +111,45 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr int kMergeRegs = 8;  // segments a merge folds from registers
 
 // Merges of the sequences queued in `list` (rows of sequence, w_lo, w_hi), all at once.
-// An item is 4 consecutive output dims of one head of one queued sequence; each thread
-// takes two items per round and issues both items' loads before folding either, so the
-// whole queue costs about one memory latency per 2 * blockDim.x items.  Sequences with
-// more than kMergeRegs segments are merged afterwards from global memory.
+// An item is 8 consecutive output dims of one head of one queued sequence; each thread takes
+// one item per round.  A wave loads only as many segments as the longest sequence among its
+// items has (a wave-uniform bound, so the loads need no divergent branch), and every load is
+// issued before any fold, so the queue costs about one memory latency per blockDim.x items.
+// Sequences with more than kMergeRegs segments are merged afterwards from global memory.
 template <typename T, int D>
 struct MergeItem {
   float2 ml[kMergeRegs];
-  float4 po[kMergeRegs];
+  float4 po[kMergeRegs][2];
   int b = -1, h = 0, d = 0, nseg = 0;
-  // Item `item` of `nitems` (>= 1).  Every load is issued, from clamped indices, whether or
-  // not the item is real (item >= nitems) or short of kMergeRegs segments: a load under a
-  // branch gets a wait for its result at the branch's end, which would serialise them.
-  __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int per, int item,
-                                       int nitems) {
+  // Item `item` of `nitems` (>= 1): which sequence, head and dims, and its segment count
+  // (capped at kMergeRegs).  Items past the end repeat the last one and are not stored.
+  __device__ __forceinline__ int locate(const int (*list)[3], int per, int item, int nitems) {
     const bool real = item < nitems;
     const int it = real ? item : nitems - 1;
     const int i = it / per, r = it - i * per;
-    const int bb = list[i][0], lo = list[i][1];
-    nseg = list[i][2] - lo + 1;
-    b = (real && nseg <= kMergeRegs) ? bb : -1;  // longer ones are merged from global memory
+    nseg = list[i][2] - list[i][1] + 1;
+    b = (real && nseg <= kMergeRegs) ? list[i][0] : -1;  // longer ones are merged from global memory
+    h = r / (D / 8);
+    d = (r - h * (D / 8)) * 8;
+    return i;
+  }
+  // Loads of segments 0 .. nsw - 1 (nsw wave-uniform, >= this item's capped segment count),
+  // from clamped indices.
+  __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int i, int nsw) {
     const int ns = nseg < kMergeRegs ? nseg : kMergeRegs;
-    h = r / (D / 4);
-    d = (r - h * (D / 4)) * 4;
-    const int64_t s0 = (int64_t)(lo + bb) * P.hq + h;
+    const int64_t s0 = (int64_t)(list[i][1] + list[i][0]) * P.hq + h;
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
-      const int64_t e = s0 + (int64_t)(s < ns ? s : ns - 1) * P.hq;
-      ml[s] = P.part_ml[e];
-      po[s] = *reinterpret_cast<const float4*>(P.part_o + e * D + d);
+      if (s < nsw) {
+        const int64_t e = s0 + (int64_t)(s < ns ? s : ns - 1) * P.hq;
+        ml[s] = P.part_ml[e];
+        const float4* src = reinterpret_cast<const float4*>(P.part_o + e * D + d);
+        po[s][0] = src[0];
+        po[s][1] = src[1];
+      } else {  // (never selected by finish: set so that no value is left undefined)
+        ml[s] = make_float2(-INFINITY, 0.f);
+        po[s][0] = po[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
   }
   __device__ __forceinline__ void finish(const DecodeParams& P) const {
@@ -148,7 +158,7 @@ struct MergeItem {
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) M = s < nseg ? fmaxf(M, ml[s].x) : M;
     float den = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
       const float c = (s < nseg && ml[s].y > 0.f) ? exp2f(ml[s].x - M) * ml[s].y : 0.f;
@@ -157,22 +167,23 @@ struct MergeItem {
       // value used only under a branch lets the compiler sink its load into that branch,
       // where it is issued late and waited for at once.
       const bool use = c != 0.f;
-      acc.x += use ? c * po[s].x : 0.f;
-      acc.y += use ? c * po[s].y : 0.f;
-      acc.z += use ? c * po[s].z : 0.f;
-      acc.w += use ? c * po[s].w : 0.f;
+      const float v[8] = {po[s][0].x, po[s][0].y, po[s][0].z, po[s][0].w,
+                          po[s][1].x, po[s][1].y, po[s][1].z, po[s][1].w};
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] += use ? c * v[x] : 0.f;
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
     T* orow = reinterpret_cast<T*>(P.out) + b * P.o_sn + h * P.o_sh + d;
     if (sizeof(T) == 2 && P.o_vec) {
-      T v[4] = {from_f32<T>(acc.x * inv), from_f32<T>(acc.y * inv), from_f32<T>(acc.z * inv),
-                from_f32<T>(acc.w * inv)};
-      *reinterpret_cast<uint2*>(orow) = *reinterpret_cast<const uint2*>(v);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        T v[4] = {from_f32<T>(acc[4 * half] * inv), from_f32<T>(acc[4 * half + 1] * inv),
+                  from_f32<T>(acc[4 * half + 2] * inv), from_f32<T>(acc[4 * half + 3] * inv)};
+        *reinterpret_cast<uint2*>(orow + 4 * half) = *reinterpret_cast<const uint2*>(v);
+      }
     } else {
-      orow[0] = from_f32<T>(acc.x * inv);
-      orow[1] = from_f32<T>(acc.y * inv);
-      orow[2] = from_f32<T>(acc.z * inv);
-      orow[3] = from_f32<T>(acc.w * inv);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) orow[x] = from_f32<T>(acc[x] * inv);
     }
   }
 };
@@ -182,26 +193,27 @@ __device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int
 
 template <typename T, int D>
 __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*list)[3], int nm) {
-  const int per = P.hq * (D / 4);
+  const int per = P.hq * (D / 8);
   const int nitems = nm * per;
   const int nt = blockDim.x;
   auto round = [&](int base) __attribute__((always_inline)) {
-    const int i0 = base + threadIdx.x, i1 = i0 + nt;
-    MergeItem<T, D> a, c;
-    a.load(P, list, per, i0, nitems);
-    c.load(P, list, per, i1, nitems);
-    asm volatile("" ::: "memory");  // both items' loads are issued before either fold
+    MergeItem<T, D> a;
+    const int i = a.locate(list, per, base + threadIdx.x, nitems);
+    int nsw = a.nseg < kMergeRegs ? a.nseg : kMergeRegs;  // the wave's longest item
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) nsw = max(nsw, __shfl_xor(nsw, off, 64));
+    a.load(P, list, i, __builtin_amdgcn_readfirstlane(nsw));
+    asm volatile("" ::: "memory");  // every load is issued before the fold
     a.finish(P);
-    c.finish(P);
   };
-  // The first round (all of it when nitems <= 2 * blockDim.x, the usual case) is peeled off
-  // the loop: inside a loop, registers that the previous round's loads filled can make the
+  // The first round (all of it when nitems <= blockDim.x, the usual case) is peeled off the
+  // loop: inside a loop, registers that the previous round's loads filled can make the
   // compiler wait for those loads before issuing the next ones.  With no items (nm == 0:
   // this workgroup arrived last for none of its splits) nothing runs: an item's loads use
   // list rows that only exist when nitems > 0.
   if (nitems <= 0) return;
   round(0);
-  for (int base = 2 * nt; base < nitems; base += 2 * nt) round(base);
+  for (int base = nt; base < nitems; base += nt) round(base);
   for (int i = 0; i < nm; ++i)
     if (list[i][2] - list[i][1] + 1 > kMergeRegs) merge_partials<T, D>(P, list[i][0], list[i][1], list[i][2]);
 }
