@@ -62,6 +62,12 @@ __global__ void append_kernel(const char* __restrict__ k, int64_t k_sn, int64_t 
     r /= hkv;
     int kv = (int)(r & 1);
     int i = (int)(r >> 1);
+    // The source chunk is read first, in parallel with the page-table lookups below (it does
+    // not depend on them); the empty asm keeps the compiler from sinking the load into the
+    // store's branch, which would chain it behind the lookups.
+    const char* src = (kv ? v + i * v_sn + h * v_sh : k + i * k_sn + h * k_sh) + c * VEC;
+    const V val = *reinterpret_cast<const V*>(src);
+    asm volatile("" ::: "memory");
     int b = bidx[i];
     int p = pos[i];
     bool ok = b >= 0 && b < batch && p >= 0;
@@ -81,10 +87,9 @@ __global__ void append_kernel(const char* __restrict__ k, int64_t k_sn, int64_t 
       continue;
     }
     int slot = p % ps;
-    const char* src = (kv ? v + i * v_sn + h * v_sh : k + i * k_sn + h * k_sh) + c * VEC;
     char* dst = (kv ? v_cache : k_cache) + page * page_stride +
                 ((int64_t)slot * hkv + h) * row_bytes + c * VEC;
-    *reinterpret_cast<V*>(dst) = *reinterpret_cast<const V*>(src);
+    *reinterpret_cast<V*>(dst) = val;
   }
 }
 

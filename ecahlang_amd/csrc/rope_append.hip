@@ -62,16 +62,23 @@ struct Run {
   }
 };
 
+// The token's cos / sin at dims d0.. and d0 + D/2..
+template <typename T, int N, bool VEC>
+struct CosSin {
+  Run<T, N, VEC> c0, c1, s0, s1;
+  __device__ __forceinline__ void load(const T* cs, const T* sn, int half) {
+    c0.load(cs);
+    c1.load(cs + half);
+    s0.load(sn);
+    s1.load(sn + half);
+  }
+};
+
 // lo / hi: dims d0.. and d0 + D/2.. of one row, rotated in place with the token's cos / sin.
 template <typename T, int N, bool VEC>
-__device__ __forceinline__ void rotate(Run<T, N, VEC>& lo, Run<T, N, VEC>& hi, const T* cs, const T* sn,
-                                       int half) {
+__device__ __forceinline__ void rotate(Run<T, N, VEC>& lo, Run<T, N, VEC>& hi, const CosSin<T, N, VEC>& t) {
 #pragma clang fp contract(off)
-  Run<T, N, VEC> c0, c1, s0, s1;
-  c0.load(cs);
-  c1.load(cs + half);
-  s0.load(sn);
-  s1.load(sn + half);
+  const Run<T, N, VEC>&c0 = t.c0, &c1 = t.c1, &s0 = t.s0, &s1 = t.s1;
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     const float a = to_f32(lo.e[j]), b = to_f32(hi.e[j]);
@@ -102,11 +109,13 @@ __global__ void rope_append_kernel(const T* q, int64_t q_sn, int64_t q_sh, T* q_
     const int row = (int)(r0 % rows);
     const int64_t i = r0 / rows;
     Run<T, N, VEC> lo, hi;
+    CosSin<T, N, VEC> cs;
     if (row < hq) {  // query row: rotated into q_out
       const T* src = q + i * q_sn + row * q_sh + d0;
       lo.load(src);
       hi.load(src + half);
-      rotate(lo, hi, cos_ + i * cs_sn + d0, sin_ + i * cs_sn + d0, half);
+      cs.load(cos_ + i * cs_sn + d0, sin_ + i * cs_sn + d0, half);
+      rotate(lo, hi, cs);
       T* dst = q_out + i * qo_sn + row * qo_sh + d0;
       lo.store(dst);
       hi.store(dst + half);
@@ -114,6 +123,14 @@ __global__ void rope_append_kernel(const T* q, int64_t q_sn, int64_t q_sh, T* q_
     }
     const bool is_v = row - hq >= hkv;
     const int h = is_v ? row - hq - hkv : row - hq;
+    // The row and the token's cos / sin (read for value rows too, unused, so that no load
+    // sits under a divergent branch) are requested before the page-table lookups, which they
+    // do not depend on; the empty asm keeps the compiler from sinking them behind those.
+    const T* src = is_v ? v + i * v_sn + h * v_sh + d0 : k + i * k_sn + h * k_sh + d0;
+    lo.load(src);
+    hi.load(src + half);
+    cs.load(cos_ + i * cs_sn + d0, sin_ + i * cs_sn + d0, half);
+    asm volatile("" ::: "memory");
     const int b = bidx[i], p = pos[i];
     bool ok = b >= 0 && b < batch && p >= 0;
     int page = -1;
@@ -129,11 +146,8 @@ __global__ void rope_append_kernel(const T* q, int64_t q_sn, int64_t q_sh, T* q_
       if (row == hq && d0 == 0 && err) atomicAdd(err, 1);
       continue;
     }
-    const T* src = is_v ? v + i * v_sn + h * v_sh + d0 : k + i * k_sn + h * k_sh + d0;
     T* dst = (is_v ? v_cache : k_cache) + page * page_stride + ((int64_t)(p % ps) * hkv + h) * d + d0;
-    lo.load(src);
-    hi.load(src + half);
-    if (!is_v) rotate(lo, hi, cos_ + i * cs_sn + d0, sin_ + i * cs_sn + d0, half);
+    if (!is_v) rotate(lo, hi, cs);
     lo.store(dst);
     hi.store(dst + half);
   }
