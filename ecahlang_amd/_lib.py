@@ -29,6 +29,8 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _vp, _i64, _vp,
          _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     ),
+    "pkv_append_paged_kv_cache_slots": (
+        _i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pkv_append_paged_kv_cache_rope": (
         _i32,
         [_vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
@@ -49,7 +51,7 @@ SIGNATURES: dict[str, tuple] = {
          _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
     ),
     "pkv_pool_apply": (_i32, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _vp, _vp]),
-    "pkv_pool_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _vp, _vp]),
+    "pkv_pool_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp]),
     "pkv_top_k_top_p_sampling": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp]),
     "pkv_sampling_workspace_bytes": (_i64, [_i32, _i32]),
     "pkv_top_k_top_p_sampling_ws": (

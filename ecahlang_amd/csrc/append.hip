@@ -3,6 +3,8 @@
 //   pkv_get_seq_lens                 <- flashinfer.get_seq_lens              (ecahlang/manager.py:143, 170)
 //   pkv_get_batch_indices_positions  <- flashinfer.get_batch_indices_positions (ecahlang/manager.py:144-146, 171-173)
 //   pkv_append_paged_kv_cache        <- flashinfer.page.append_paged_kv_cache (ecahlang/manager.py:155-165, 175-185, 271-280)
+//   pkv_append_paged_kv_cache_slots  <- the same append with each token's slot resolved beforehand
+//                                       (the CUDA-graph decode step, ecahlang/manager.py:270-280)
 //
 // The append is pure data movement: every byte of the new K/V rows lands, unchanged, in
 // cache[page][kv][slot][head][:] with page = kv_indices[kv_indptr[b] + pos / page_size] and
@@ -40,7 +42,10 @@ __global__ void batch_positions_kernel(const int32_t* __restrict__ append_indptr
 
 // One lane per VEC-byte chunk of a (token, k|v, head) row.  Index order, fastest first:
 // chunk, head, k|v, token -- destination rows of consecutive heads are adjacent in a slot.
-template <int VEC>
+// With SLOTS, token i's destination is slots[i] = page * ps + slot (from the page-table gather),
+// one lookup instead of the three dependent ones through batch_indices / positions, kv_indptr
+// and kv_indices.
+template <int VEC, bool SLOTS>
 __global__ void append_kernel(const char* __restrict__ k, int64_t k_sn, int64_t k_sh,
                               const char* __restrict__ v, int64_t v_sn, int64_t v_sh,
                               const int32_t* __restrict__ bidx, const int32_t* __restrict__ pos,
@@ -48,7 +53,8 @@ __global__ void append_kernel(const char* __restrict__ k, int64_t k_sn, int64_t 
                               int64_t page_stride, int64_t num_pages,
                               const int32_t* __restrict__ kv_indices, int64_t num_indices,
                               const int32_t* __restrict__ kv_indptr, int32_t batch, int32_t hkv,
-                              int32_t row_bytes, int32_t ps, int32_t* __restrict__ err) {
+                              int32_t row_bytes, int32_t ps, const int32_t* __restrict__ slots,
+                              int32_t* __restrict__ err) {
   using V = typename std::conditional<VEC == 16, uint4,
             typename std::conditional<VEC == 8, uint2,
             typename std::conditional<VEC == 4, uint32_t, uint16_t>::type>::type>::type;
@@ -68,25 +74,33 @@ __global__ void append_kernel(const char* __restrict__ k, int64_t k_sn, int64_t 
     const char* src = (kv ? v + i * v_sn + h * v_sh : k + i * k_sn + h * k_sh) + c * VEC;
     const V val = *reinterpret_cast<const V*>(src);
     asm volatile("" ::: "memory");
-    int b = bidx[i];
-    int p = pos[i];
-    bool ok = b >= 0 && b < batch && p >= 0;
-    int page = -1;
-    if (ok) {
-      int base = kv_indptr[b];
-      int np = kv_indptr[b + 1] - base;
-      int pi = p / ps;
-      ok = pi < np && (int64_t)base + pi < num_indices;
+    bool ok;
+    int page = -1, slot = 0;
+    if constexpr (SLOTS) {
+      const int sl = slots[i];
+      ok = sl >= 0 && sl / ps < num_pages;
+      page = sl / ps;
+      slot = sl - page * ps;
+    } else {
+      int b = bidx[i];
+      int p = pos[i];
+      ok = b >= 0 && b < batch && p >= 0;
       if (ok) {
-        page = kv_indices[base + pi];
-        ok = page >= 0 && page < num_pages;
+        int base = kv_indptr[b];
+        int np = kv_indptr[b + 1] - base;
+        int pi = p / ps;
+        ok = pi < np && (int64_t)base + pi < num_indices;
+        if (ok) {
+          page = kv_indices[base + pi];
+          ok = page >= 0 && page < num_pages;
+        }
       }
+      slot = p % ps;
     }
     if (!ok) {  // metadata that points outside the sequence's pages: skip, count it
       if (c == 0 && err) atomicAdd(err, 1);
       continue;
     }
-    int slot = p % ps;
     char* dst = (kv ? v_cache : k_cache) + page * page_stride +
                 ((int64_t)slot * hkv + h) * row_bytes + c * VEC;
     *reinterpret_cast<V*>(dst) = val;
@@ -118,13 +132,14 @@ extern "C" int pkv_get_batch_indices_positions(const int32_t* append_indptr,
   return (int)hipGetLastError();
 }
 
-extern "C" int pkv_append_paged_kv_cache(
-    const void* append_key, int64_t k_stride_n, int64_t k_stride_h, const void* append_value,
-    int64_t v_stride_n, int64_t v_stride_h, const int32_t* batch_indices, const int32_t* positions,
-    int32_t nnz, void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
-    const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr, int32_t batch,
-    int32_t num_kv_heads,
-    int32_t head_dim, int32_t page_size, int32_t dtype, int32_t* err_count, void* stream) {
+namespace {
+
+int launch_append(const void* append_key, int64_t k_stride_n, int64_t k_stride_h, const void* append_value,
+                  int64_t v_stride_n, int64_t v_stride_h, const int32_t* batch_indices, const int32_t* positions,
+                  const int32_t* slots, int32_t nnz, void* k_cache, void* v_cache, int64_t page_stride,
+                  int64_t num_pages, const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr,
+                  int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t dtype,
+                  int32_t* err_count, void* stream) {
   int es = dtype == kF32 ? 4 : (dtype == kF16 || dtype == kBF16) ? 2 : 0;
   if (!es) return kBadDType;
   if (nnz < 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || batch < 0) return kBadArg;
@@ -146,19 +161,53 @@ extern "C" int pkv_append_paged_kv_cache(
   int64_t want = (total + threads - 1) / threads;
   int blocks = (int)(want < 65536 ? want : 65536);
   hipStream_t s = (hipStream_t)stream;
-#define PKV_APPEND(VB)                                                                          \
-  hipLaunchKernelGGL(append_kernel<VB>, dim3(blocks), dim3(threads), 0, s,                      \
+#define PKV_APPEND(VB, SL)                                                                      \
+  hipLaunchKernelGGL((append_kernel<VB, SL>), dim3(blocks), dim3(threads), 0, s,                \
                      (const char*)append_key, ksn, ksh, (const char*)append_value, vsn, vsh,    \
                      batch_indices, positions, nnz, (char*)k_cache, (char*)v_cache, pstride,    \
                      num_pages, kv_indices, num_indices, kv_indptr, batch, num_kv_heads,        \
-                     row_bytes,                                                                 \
-                     page_size, err_count)
-  switch (vec) {
-    case 16: PKV_APPEND(16); break;
-    case 8: PKV_APPEND(8); break;
-    case 4: PKV_APPEND(4); break;
-    default: PKV_APPEND(2); break;
+                     row_bytes, page_size, slots, err_count)
+  if (slots) {
+    switch (vec) {
+      case 16: PKV_APPEND(16, true); break;
+      case 8: PKV_APPEND(8, true); break;
+      case 4: PKV_APPEND(4, true); break;
+      default: PKV_APPEND(2, true); break;
+    }
+  } else {
+    switch (vec) {
+      case 16: PKV_APPEND(16, false); break;
+      case 8: PKV_APPEND(8, false); break;
+      case 4: PKV_APPEND(4, false); break;
+      default: PKV_APPEND(2, false); break;
+    }
   }
 #undef PKV_APPEND
   return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int pkv_append_paged_kv_cache(
+    const void* append_key, int64_t k_stride_n, int64_t k_stride_h, const void* append_value,
+    int64_t v_stride_n, int64_t v_stride_h, const int32_t* batch_indices, const int32_t* positions,
+    int32_t nnz, void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
+    const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr, int32_t batch,
+    int32_t num_kv_heads,
+    int32_t head_dim, int32_t page_size, int32_t dtype, int32_t* err_count, void* stream) {
+  if (nnz > 0 && (!batch_indices || !positions)) return kBadArg;
+  return launch_append(append_key, k_stride_n, k_stride_h, append_value, v_stride_n, v_stride_h, batch_indices,
+                       positions, nullptr, nnz, k_cache, v_cache, page_stride, num_pages, kv_indices, num_indices,
+                       kv_indptr, batch, num_kv_heads, head_dim, page_size, dtype, err_count, stream);
+}
+
+extern "C" int pkv_append_paged_kv_cache_slots(
+    const void* append_key, int64_t k_stride_n, int64_t k_stride_h, const void* append_value,
+    int64_t v_stride_n, int64_t v_stride_h, const int32_t* slots, int32_t nnz, void* k_cache, void* v_cache,
+    int64_t page_stride, int64_t num_pages, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+    int32_t dtype, int32_t* err_count, void* stream) {
+  if (nnz > 0 && !slots) return kBadArg;
+  return launch_append(append_key, k_stride_n, k_stride_h, append_value, v_stride_n, v_stride_h, nullptr, nullptr,
+                       slots, nnz, k_cache, v_cache, page_stride, num_pages, nullptr, 0, nullptr, 0, num_kv_heads,
+                       head_dim, page_size, dtype, err_count, stream);
 }

@@ -57,12 +57,24 @@ __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* t
 
 // indices[indptr[b] + k] = table[desc[4b]][desc[4b+1] + k] for k < desc[4b+2]; one thread per
 // output entry finds its sequence by binary search over indptr.
+// With `slots`, also each row's append slot: slots[b] = page * ps + positions[b] % ps for the
+// page holding position positions[b] of row b, or -1 when that position is outside the row's
+// pages (rows with no pages included: a thread per row writes the -1s, the thread gathering
+// the page writes the rest).
 __global__ void pool_gather_kernel(const int32_t* table, int64_t stride, int32_t rows, const int32_t* desc,
                                    const int32_t* indptr, int32_t batch, int32_t* indices,
-                                   int64_t num_indices, int32_t* err) {
+                                   int64_t num_indices, const int32_t* positions, int32_t ps,
+                                   int32_t* slots, int32_t* err) {
   const int64_t total = indptr[batch] < num_indices ? indptr[batch] : num_indices;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+  const int64_t span = total > batch || !slots ? total : batch;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < span;
        t += (int64_t)gridDim.x * blockDim.x) {
+    if (slots && t < batch) {
+      const int p = positions[t];
+      const int64_t np = (int64_t)indptr[t + 1] - indptr[t];
+      if (p < 0 || p / ps >= np || (int64_t)indptr[t] + p / ps >= total) slots[t] = -1;
+    }
+    if (t >= total) continue;
     int lo = 0, hi = batch;  // largest b with indptr[b] <= t
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
@@ -70,11 +82,16 @@ __global__ void pool_gather_kernel(const int32_t* table, int64_t stride, int32_t
     }
     const int row = desc[4 * lo], col = desc[4 * lo + 1], n = desc[4 * lo + 2];
     const int64_t k = t - indptr[lo];
+    int page = -1;
     if (row >= 0 && row < rows && k < n && col + k < stride) {
-      indices[t] = table[(int64_t)row * stride + col + k];
-    } else {
-      indices[t] = -1;
-      if (err) atomicAdd(err, 1);
+      page = table[(int64_t)row * stride + col + k];
+    } else if (err) {
+      atomicAdd(err, 1);
+    }
+    indices[t] = page;
+    if (slots) {
+      const int p = positions[lo];
+      if (p >= 0 && p / ps == k) slots[lo] = page < 0 ? -1 : page * ps + p % ps;
     }
   }
 }
@@ -93,14 +110,18 @@ extern "C" int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table
 
 extern "C" int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t rows, const int32_t* desc,
                                const int32_t* indptr, int32_t batch, int32_t* indices,
-                               int64_t num_indices, int64_t max_total, int32_t* err, void* stream) {
+                               int64_t num_indices, int64_t max_total, const int32_t* positions,
+                               int32_t page_size, int32_t* slots, int32_t* err, void* stream) {
   if (batch < 0 || stride <= 0 || rows <= 0 || num_indices < 0 || max_total < 0) return kBadArg;
-  if (batch == 0 || max_total == 0) return kOk;
-  const int64_t n = max_total < num_indices ? max_total : num_indices;
+  if (slots && (!positions || page_size <= 0)) return kBadArg;
+  if (batch == 0 || (max_total == 0 && !slots)) return kOk;
+  int64_t n = max_total < num_indices ? max_total : num_indices;
+  if (slots && n < batch) n = batch;
   const int threads = 256;
   int64_t blocks = (n + threads - 1) / threads;
   blocks = blocks < 1024 ? (blocks > 0 ? blocks : 1) : 1024;
   hipLaunchKernelGGL(pool_gather_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream,
-                     table, stride, rows, desc, indptr, batch, indices, num_indices, err);
+                     table, stride, rows, desc, indptr, batch, indices, num_indices, positions, page_size,
+                     slots, err);
   return (int)hipGetLastError();
 }

@@ -44,7 +44,8 @@ import numpy as np
 import torch
 
 from ._lib import check, lib, stream_ptr
-from .ops import append_paged_kv_cache, get_batch_indices_positions, get_seq_lens
+from .ops import (append_paged_kv_cache, append_paged_kv_cache_slots, get_batch_indices_positions,
+                  get_seq_lens)
 
 _POP, _PUSH, _COPY = 0, 1, 2
 
@@ -227,6 +228,7 @@ class AutoKVCacheManager:
         self._cg_positions: dict = {}
         self._cg_append_indptr: dict = {}
         self._cg_meta: dict = {}  # bucket -> [desc | indptr | last_page_len | positions] (the three are views)
+        self._cg_slots: dict = {}  # bucket -> each row's append slot, page * block_size + position % block_size
         # The pool's initial state (free stack, page table, cache) is written on the current
         # stream; a caller may go on to drive the pool from another stream, so it is complete
         # before the constructor returns.
@@ -289,16 +291,23 @@ class AutoKVCacheManager:
         return slot, out, b, int(indptr[-1])
 
     def _gather(self, slot: int, staged: np.ndarray, b: int, pages: int, out_indices: torch.Tensor,
-                dst: torch.Tensor | None = None) -> torch.Tensor:
+                dst: torch.Tensor | None = None, slots: torch.Tensor | None = None) -> torch.Tensor:
         """Copy the staged [desc | indptr | extra] to the device (into ``dst`` when given) and
-        gather out_indices[indptr[r] + k] = table[desc...]; returns the device [indptr | extra]."""
+        gather out_indices[indptr[r] + k] = table[desc...]; returns the device [indptr | extra].
+        With ``slots``, extra is [last_page_len | positions] and each row's append slot
+        (page * block_size + position % block_size) is written there too."""
         self._flush()
         dev = self._staging.send(slot, staged, dst)
         d_desc, d_rest = dev[: 4 * b], dev[4 * b:]
-        if pages:
+        if pages or slots is not None:
+            pos_ptr, slots_ptr = 0, 0
+            if slots is not None:
+                pos_ptr = d_rest[2 * b + 1:].data_ptr()
+                slots_ptr = slots.data_ptr()
             check(lib().pkv_pool_gather(self._table.data_ptr(), self._stride, self._rows, d_desc.data_ptr(),
                                         d_rest.data_ptr(), b, out_indices.data_ptr(), out_indices.numel(),
-                                        pages, self._err.data_ptr(), stream_ptr(self.device)),
+                                        pages, pos_ptr, self.block_size, slots_ptr, self._err.data_ptr(),
+                                        stream_ptr(self.device)),
                   "page table gather")
         return d_rest
 
@@ -478,6 +487,7 @@ class AutoKVCacheManager:
             self._cg_kv_last_page_len[bs] = meta[5 * bs + 1: 6 * bs + 1]
             self._cg_batch_indices[bs] = torch.arange(bs, dtype=torch.int32, device=dev)
             self._cg_positions[bs] = meta[6 * bs + 1: 7 * bs + 1]
+            self._cg_slots[bs] = torch.full((bs,), -1, dtype=torch.int32, device=dev)
             self._cg_append_indptr[bs] = torch.arange(bs + 1, dtype=torch.int32, device=dev)
             self._cg_temperature[bs] = torch.ones(bs, 1, dtype=torch.float32, device=dev)
             self._cg_top_k[bs] = torch.full((bs,), self.vocab_size, dtype=torch.int32, device=dev)
@@ -494,18 +504,16 @@ class AutoKVCacheManager:
             raise RuntimeError("page table larger than the bucket's kv_indices buffer")
         # [desc | indptr | last | positions] lands in the bucket's block: the three buffers the
         # captured step reads are views of it
-        self._gather(slot, staged, b, pages, self._cg_kv_indices[bucket_size], dst=self._cg_meta[bucket_size])
+        self._gather(slot, staged, b, pages, self._cg_kv_indices[bucket_size], dst=self._cg_meta[bucket_size],
+                     slots=self._cg_slots[bucket_size])
 
     def append_paged_kv_cache_cuda_graph(self, key, value, bucket_size: int, layer_idx: int) -> None:
-        """manager.py:270-280."""
-        append_paged_kv_cache(append_key=key, append_value=value,
-                              batch_indices=self._cg_batch_indices[bucket_size],
-                              positions=self._cg_positions[bucket_size],
-                              paged_kv_cache=self.kv_cache[layer_idx],
-                              kv_indices=self._cg_kv_indices[bucket_size],
-                              kv_indptr=self._cg_kv_indptr[bucket_size],
-                              kv_last_page_len=self._cg_kv_last_page_len[bucket_size],
-                              kv_layout=self.layout)
+        """manager.py:270-280: the append through the bucket's static metadata.  Each row's
+        destination (the page and slot its ``positions`` entry selects through ``kv_indptr`` /
+        ``kv_indices``) is resolved once per step by ``fill_cuda_graph_metadata``, so every
+        layer's append reads one slot per token."""
+        append_paged_kv_cache_slots(key, value, self._cg_slots[bucket_size], self.kv_cache[layer_idx],
+                                    kv_layout=self.layout)
 
     # ------------------------------------------------------------------ sampling buffers (outside the path)
     # main.py reads sampling_{temperature,top_k,top_p}_gpu and the bucket's _cg_* copies of

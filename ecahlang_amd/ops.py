@@ -147,6 +147,39 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
         stream_ptr(cv.device)), "append_paged_kv_cache")
 
 
+def append_paged_kv_cache_slots(append_key: torch.Tensor, append_value: torch.Tensor, slots: torch.Tensor,
+                                paged_kv_cache: CacheT, kv_layout: str = "NHD",
+                                err_count: torch.Tensor | None = None) -> None:
+    """``append_paged_kv_cache`` with each token's destination resolved beforehand: token i goes
+    to page ``slots[i] // ps``, slot ``slots[i] % ps`` (``slots`` as the page-table gather of
+    ``AutoKVCacheManager.fill_cuda_graph_metadata`` writes them).  One lookup per token instead
+    of the three dependent ones through batch_indices / positions, kv_indptr and kv_indices;
+    the bytes written are the same.  Tokens with a negative or out-of-pool slot are skipped and
+    counted in ``err_count``.
+    """
+    cv = CacheView(paged_kv_cache, kv_layout)
+    for t, n in ((append_key, "append_key"), (append_value, "append_value")):
+        if t.dtype != cv.dtype:
+            raise ValueError(f"{n} dtype {t.dtype} differs from the cache dtype {cv.dtype}")
+        if t.shape[1:] != (cv.num_kv_heads, cv.head_dim):
+            raise ValueError(f"{n} must be [nnz, {cv.num_kv_heads}, {cv.head_dim}]")
+    nnz = append_key.shape[0]
+    if append_value.shape[0] != nnz or slots.numel() < nnz:
+        raise ValueError("append_key, append_value and slots disagree on nnz")
+    _i32(slots, "slots")
+    ksn, ksh = _row_strides(append_key, "append_key")
+    vsn, vsh = _row_strides(append_value, "append_value")
+    err_ptr = 0
+    if err_count is not None:
+        err_ptr = _i32(err_count, "err_count").data_ptr()
+    if nnz == 0:
+        return
+    check(lib().pkv_append_paged_kv_cache_slots(
+        append_key.data_ptr(), ksn, ksh, append_value.data_ptr(), vsn, vsh, slots.data_ptr(), nnz,
+        cv.k_ptr, cv.v_ptr, cv.page_stride, cv.num_pages, cv.num_kv_heads, cv.head_dim, cv.page_size,
+        dtype_code(cv.dtype), err_ptr, stream_ptr(cv.device)), "append_paged_kv_cache_slots")
+
+
 def append_paged_kv_cache_with_rope(q: torch.Tensor, append_key: torch.Tensor, append_value: torch.Tensor,
                                     cos: torch.Tensor, sin: torch.Tensor, batch_indices: torch.Tensor,
                                     positions: torch.Tensor, paged_kv_cache: CacheT,

@@ -66,6 +66,20 @@ int pkv_append_paged_kv_cache(const void* append_key, int64_t k_stride_n, int64_
                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                               int32_t dtype, int32_t* err_count, void* stream);
 
+/* The same append with each token's destination resolved beforehand: token i goes to page
+ * slots[i] / page_size, slot slots[i] % page_size (slots as pkv_pool_gather writes them).  What
+ * the CUDA-graph decode step's append (ecahlang/manager.py:270-280, the reference's
+ * append_paged_kv_cache with the bucket's static batch_indices / positions / kv_indptr /
+ * kv_indices) computes, with one lookup per token instead of three dependent ones.  A slot
+ * that is negative or outside the num_pages-page pool is skipped and counted in *err_count
+ * (may be NULL). */
+int pkv_append_paged_kv_cache_slots(const void* append_key, int64_t k_stride_n, int64_t k_stride_h,
+                                    const void* append_value, int64_t v_stride_n, int64_t v_stride_h,
+                                    const int32_t* slots, int32_t nnz, void* k_cache, void* v_cache,
+                                    int64_t page_stride, int64_t num_pages, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t page_size, int32_t dtype,
+                                    int32_t* err_count, void* stream);
+
 /* The model's rotary embedding on the new tokens' q and k, then the append, in one launch:
  * apply_rotary_pos_emb (transformers/models/qwen2/modeling_qwen2.py:210-211, run just before
  * the attention hook) followed by the hook's append (ecahlang/main.py:62-66 ->
@@ -184,10 +198,15 @@ int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t s
  * :231-246): kv_indices[indptr[b] + k] = table[desc[4b]][desc[4b+1] + k] for k < desc[4b+2],
  * with indptr[batch+1] (the exclusive scan of the desc counts) already on the device.  At most
  * min(max_total, num_indices) entries are written; entries with no source are set to -1 and
- * counted in *err (may be NULL). */
+ * counted in *err (may be NULL).  With slots (may be NULL; then positions and page_size are
+ * unused), also slots[b] = page * page_size + positions[b] % page_size, where page is the
+ * gathered id at position positions[b] of row b, or -1 when that position lies outside the
+ * row's gathered pages: the destinations pkv_append_paged_kv_cache_slots takes (the slot that
+ * append_paged_kv_cache_cuda_graph, manager.py:270-280, resolves on every layer). */
 int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t rows, const int32_t* desc,
                     const int32_t* indptr, int32_t batch, int32_t* kv_indices, int64_t num_indices,
-                    int64_t max_total, int32_t* err, void* stream);
+                    int64_t max_total, const int32_t* positions, int32_t page_size, int32_t* slots,
+                    int32_t* err, void* stream);
 
 /* Top-k / top-p sampling from logits (flashinfer.sampling.top_k_top_p_sampling_from_logits at
  * ecahlang/main.py:377-379, 400-402, 489-491, 582-584: top-k first, then top-p on the

@@ -163,6 +163,48 @@ def test_append_out_of_range_metadata_is_skipped_and_counted():
     assert err.item() > 0
 
 
+def _host_slots(wb):
+    ind, ptr, ps = wb.indices.tolist(), wb.indptr.tolist(), wb.ps
+    return torch.tensor([ind[ptr[b] + p // ps] * ps + p % ps
+                         for b, p in zip(wb.batch_indices.tolist(), wb.positions.tolist())], dtype=torch.int32)
+
+
+@pytest.mark.parametrize("name", list(APPEND_CASES))
+def test_append_by_slot_bit_exact_whole_pool(name):
+    wb = APPEND_CASES[name]()
+    print(f"case {name}: nnz={wb.k_new.shape[0]} pages={wb.num_pages}", flush=True)
+    want, _ = _oracle_appended(wb)
+    dv = wb.to(DEV)
+    ops.append_paged_kv_cache_slots(dv.k_new, dv.v_new, _host_slots(wb).to(DEV), dv.cache)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(dv.cache), want)
+
+
+def test_append_by_slot_misaligned_rows_and_bad_slots():
+    wb = workloads.build_batch([20, 3, 40], [2, 1, 3], 4, 2, 64, torch.float16, 12)
+    want, _ = _oracle_appended(wb)
+    dv = wb.to(DEV)
+    nnz, H, D = dv.k_new.shape
+    buf = torch.empty(2 * nnz * H * D + 1, dtype=dv.dtype, device=DEV)  # 2-byte misaligned rows
+    km = buf[1:1 + nnz * H * D].view(nnz, H, D)
+    vm = buf[1 + nnz * H * D:].view(nnz, H, D)
+    km.copy_(dv.k_new)
+    vm.copy_(dv.v_new)
+    c = dv.cache.clone()
+    ops.append_paged_kv_cache_slots(km, vm, _host_slots(wb).to(DEV), c)
+    # slots that are negative or past the pool are skipped and counted (one count per token,
+    # K or V, and head)
+    bad = torch.tensor([-1, wb.num_pages * wb.ps, 2 ** 31 - 1, -16, 0, 0], dtype=torch.int32, device=DEV)[:nnz]
+    bad[4:] = -5
+    before = _bits(dv.cache)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.append_paged_kv_cache_slots(dv.k_new, dv.v_new, bad, dv.cache, err_count=err)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(c), want)
+    assert np.array_equal(_bits(dv.cache), before)
+    assert err.item() == nnz * 2 * H
+
+
 # ---------------------------------------------------------------- decode
 
 DECODE_CASES = {

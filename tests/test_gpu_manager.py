@@ -149,6 +149,10 @@ def test_graph_buckets_match_oracle():
         assert dev._cg_kv_indptr[bucket].tolist() == ptr
         assert dev._cg_kv_last_page_len[bucket].tolist() == last
         assert dev._cg_positions[bucket].tolist() == pos
+        # each row's append slot: the page its position selects through the table, and the
+        # slot inside it (what append_paged_kv_cache_cuda_graph writes to)
+        slots = [idx[ptr[r] + p // 16] * 16 + p % 16 for r, p in enumerate(pos)]
+        assert dev._cg_slots[bucket].tolist() == slots
     with pytest.raises(RuntimeError, match="Not enough free blocks for 400 padding pages"):
         dev.init_cuda_graph_buffers([400])
     assert dev.pool_errors() == 0
