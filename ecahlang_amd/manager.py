@@ -18,7 +18,9 @@ Same constructor, methods, attribute names and exception messages as the referen
   copies (manager.py:124-137, 231-253) become one asynchronous copy of O(batch) integers and
   one kernel.  Nothing here synchronises the device except the attributes that hand page ids
   back to Python (``free_blocks`` contents, ``batch_to_blocks``, ``padding_pages``), which
-  ``main.py`` reads only for ``len(free_blocks)``.
+  ``main.py`` reads only for ``len(free_blocks)``, and the staging ring of pinned buffers
+  those copies go through, which waits for a copy only when all eight of its buffers are
+  still queued behind unfinished device work.
 
 One deliberate divergence, shared with the oracle (oracle/manager_ref.py): ``allocate(T)``
 with ``T % block_size == 0`` records ``block_size`` as the last page's length instead of 0
