@@ -390,6 +390,9 @@ PREFILL_CASES = {
     # matrix-core shapes: MHA at head_dim 64, a 16-head group, a query tile cut short
     "mha_fp16_d64": lambda: workloads.build_batch([300, 70, 513], [300, 5, 100], 8, 8, 64, torch.float16, 53),
     "g16_bf16_d64": lambda: workloads.build_batch([33, 600], [33, 40], 16, 1, 64, torch.bfloat16, 54),
+    # a request with no new tokens between two that have some (qo_indptr repeats a value)
+    "zero_chunk_bf16": lambda: workloads.build_batch([40, 200, 1, 64], [40, 0, 1, 3], 32, 8, 128,
+                                                     torch.bfloat16, 55),
 }
 
 
