@@ -568,13 +568,16 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
   };
 
   // One step: consume range page idx from the buffer, then take the head's next page and
-  // request it into the same buffer.
+  // request it into the same buffer.  The next page's id is read from LDS before the compute,
+  // so its request does not wait for that read afterwards (0.2 us per launch).
   auto step = [&](uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH], int& idx) __attribute__((always_inline)) {
     const int64_t gp = p0 + idx;
     while (gp >= seg_end) advance();
-    process(kr, vr, gp, pid_at(idx));
-    idx = grab();
-    load_page(pid_at(idx), kr, vr);
+    const int nidx = grab();
+    const int cpid = pid_at(idx), npid = pid_at(nidx);
+    process(kr, vr, gp, cpid);
+    idx = nidx;
+    load_page(npid, kr, vr);
     __builtin_amdgcn_sched_barrier(0);
   };
   start_segment();
