@@ -20,6 +20,7 @@
 // outright, so waves never combine.  An item that is one chunk of a
 // longer key range writes a partial (normalised rows plus running max and sum); the merge
 // kernel folds the partials of each split group.
+#include <type_traits>
 #include "attn_common.h"
 #include "mfma_common.h"
 #include "../../include/pagedkv.h"
@@ -73,9 +74,14 @@ struct PrefillMfmaParams {
   int64_t o_sn, o_sh;
   const int32_t* items;
   float2* part_ml;  // [slot][kRows]
-  float* part_o;    // [slot][kRows][D]
+  float* part_o;    // [slot][kRows][D] (fp16 elements for fp16 caches, else fp32)
   int32_t o_vec;
 };
+
+// Split groups' partial outputs are kept in fp16 when the cache is fp16 (averages of fp16 V
+// rows, so they fit; half the bytes written by the items and read by the merge), else fp32.
+template <typename T>
+constexpr bool kHalfPartials = std::is_same<T, _Float16>::value;
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) {
@@ -339,11 +345,19 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
       }
     } else {
       const int64_t pr = (int64_t)slot * kRows + r;
-      float* prow = P.part_o + pr * D + 4 * lg;
+      if constexpr (kHalfPartials<T>) {
+        _Float16* prow = reinterpret_cast<_Float16*>(P.part_o) + pr * D + 4 * lg;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        *reinterpret_cast<float4*>(prow + 16 * mt) = make_float4(o[rt][mt][0] * inv, o[rt][mt][1] * inv,
-                                                                 o[rt][mt][2] * inv, o[rt][mt][3] * inv);
+        for (int mt = 0; mt < MT; ++mt)
+          *reinterpret_cast<uint2*>(prow + 16 * mt) = make_uint2(Mma<T>::pack(o[rt][mt][0] * inv, o[rt][mt][1] * inv),
+                                                                 Mma<T>::pack(o[rt][mt][2] * inv, o[rt][mt][3] * inv));
+      } else {
+        float* prow = P.part_o + pr * D + 4 * lg;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          *reinterpret_cast<float4*>(prow + 16 * mt) = make_float4(o[rt][mt][0] * inv, o[rt][mt][1] * inv,
+                                                                   o[rt][mt][2] * inv, o[rt][mt][3] * inv);
+      }
       if (lg == 0) P.part_ml[pr] = make_float2(m[rt], ltot);
     }
   }
@@ -366,7 +380,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P,
   const int tt = r / G, hh = r % G;
   if (tt >= tq || ns <= 0) return;
   const float2* ml = P.part_ml + (int64_t)s0 * kRows + r;
-  const float* po = P.part_o + ((int64_t)s0 * kRows + r) * D + d;
+  const int64_t po = ((int64_t)s0 * kRows + r) * D + d;  // element offset of slot s0's dims
   float M = -INFINITY;
   for (int s = 0; s < ns; s += kMergeUnroll) {
     float2 v[kMergeUnroll];
@@ -384,7 +398,14 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P,
     for (int u = 0; u < kMergeUnroll; ++u) {
       const int64_t sl = min(s + u, ns - 1);
       w[u] = ml[sl * kRows];
-      v[u] = *reinterpret_cast<const float4*>(po + sl * kRows * D);
+      if constexpr (kHalfPartials<T>) {
+        const uint2 raw = *reinterpret_cast<const uint2*>(reinterpret_cast<const _Float16*>(P.part_o) + po + sl * kRows * D);
+        _Float16 hv[4];
+        __builtin_memcpy(hv, &raw, 8);
+        v[u] = make_float4((float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]);
+      } else {
+        v[u] = *reinterpret_cast<const float4*>(P.part_o + po + sl * kRows * D);
+      }
     }
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
