@@ -153,6 +153,14 @@ def test_graph_buckets_match_oracle():
         # slot inside it (what append_paged_kv_cache_cuda_graph writes to)
         slots = [idx[ptr[r] + p // 16] * 16 + p % 16 for r, p in enumerate(pos)]
         assert dev._cg_slots[bucket].tolist() == slots
+    # a sequence that holds no page (allocate(b, 0)) gets no slot: its position points before
+    # its pages, and the graph-bucket append skips its row, as the reference's append does
+    dev.allocate(9, 0)
+    ref.allocate(9, 0)
+    dev.fill_cuda_graph_metadata(4, [9, 3])
+    idx, ptr, last, pos = ref.fill_cuda_graph_metadata(4, [9, 3])
+    assert dev._cg_positions[4].tolist() == pos and pos[0] < 0
+    assert dev._cg_slots[4].tolist() == [-1] + [idx[ptr[r] + p // 16] * 16 + p % 16 for r, p in enumerate(pos)][1:]
     with pytest.raises(RuntimeError, match="Not enough free blocks for 400 padding pages"):
         dev.init_cuda_graph_buffers([400])
     assert dev.pool_errors() == 0
