@@ -13,7 +13,6 @@ keep that call shape:
 """
 from __future__ import annotations
 
-import heapq
 
 import math
 import os
@@ -225,8 +224,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         """The matrix-core kernel's work list.  Like FlashInfer's plan, this reads the (small)
         indptr arrays back to the host once per batch.  Items are (request, KV head, 256/g query
         tokens, chunk of the keys those tokens see); a long key range is cut into chunks so
-        that there are about one or two items per compute unit (whichever a makespan estimate
-        prefers for the batch), and the chunks' partials are merged
+        that there is about one item per compute unit, and the chunks' partials are merged
         by a second kernel.  Items are issued longest first."""
         qo = self._qo_indptr.cpu().tolist()
         kp = self._indptr.cpu().tolist()
@@ -247,28 +245,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
         total = sum(gr[3] for gr in groups)
         ncu = _num_cus(dev)
 
-        def chunk_for(per_cu: int) -> int:  # chunks are whole steps of the kernel (64 keys)
-            return max(256, min(8192, -(-total // (per_cu * ncu) // 64) * 64 or 256))
-
-        def estimate(chunk: int) -> float:
-            """Relative time of the work list: items longest first onto the least-loaded CU
-            (as the hardware dispatches them), ~3 us per item plus its keys, then the merge of
-            the split groups' slots."""
-            keys, slots = [], 0
-            for gr in groups:
-                nch = max(1, -(-gr[3] // chunk))
-                keys += [min(gr[3], (c + 1) * chunk) - c * chunk for c in range(nch)]
-                slots += nch if nch > 1 else 0
-            per_key = 0.044 * self._d / 128
-            loads = [0.0] * ncu
-            for k in sorted(keys, reverse=True):
-                heapq.heappush(loads, heapq.heappop(loads) + 3.0 + per_key * k)
-            return max(loads) + (2.0 + 0.0125 * self._d / 128 * slots if slots else 0.0)
-
-        # about one or about two items per CU, whichever the estimate prefers: fewer, longer
-        # items split fewer key ranges (less partial traffic, a shorter merge), more balance
-        # the CUs better; which wins depends on the batch's key lengths
-        chunk = min((chunk_for(1), chunk_for(2)), key=estimate)
+        # chunks are whole steps of the kernel (64 keys), sized for about one item per CU:
+        # fewer, longer items split fewer key ranges (less partial traffic, a shorter merge)
+        chunk = max(256, min(8192, -(-total // ncu // 64) * 64 or 256))
         ws_bytes = self._workspace.numel() * self._workspace.element_size()
         while True:
             items, merges, nslots = [], [], 0
