@@ -35,6 +35,25 @@ def test_python_signatures_cover_header():
     assert sorted(_lib.SIGNATURES) == _declared()
 
 
+def _declared_arity():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(pkv_[a-z0-9_]+)\s*\(([^;]*?)\)\s*;", text, flags=re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_python_argument_counts_match_header():
+    # a binding with the wrong number of arguments would pass garbage to the library on the GPU
+    from ecahlang_amd import _lib
+
+    arity = _declared_arity()
+    assert sorted(arity) == _declared()
+    wrong = {n: (len(_lib.SIGNATURES[n][1]), k) for n, k in arity.items() if len(_lib.SIGNATURES[n][1]) != k}
+    assert not wrong, wrong
+
+
 def test_loader_refuses_missing_library(monkeypatch, tmp_path):
     from ecahlang_amd import _lib
 
