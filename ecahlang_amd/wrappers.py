@@ -164,6 +164,56 @@ class BatchDecodeWithPagedKVCacheWrapper:
     forward = run
 
 
+def prefill_work_list(qo_indptr: list, kv_indptr: list, last_page_len: list, g: int, hkv: int, page_size: int,
+                      causal: bool, head_dim: int, num_cus: int, ws_bytes: int, rows: int = 256) -> dict:
+    """The matrix-core prefill kernel's work list, on the host.  Items are (request, KV head,
+    rows/g query tokens, chunk of the keys those tokens see): the 12 int32 fields
+    [b, h, t0, tq, k0, k1, slot, kv_len, qo_len, qo_start, kv_indptr[b], 0].  A key range longer
+    than the chunk is cut into chunks (slot >= 0) that form a split group
+    [first slot, chunks, qo_start, t0, tq, h, 0, 0], whose partials a second kernel merges.
+    Chunks are whole steps of the kernel (64 keys), sized for about one item per CU: fewer,
+    longer items split fewer key ranges (less partial traffic, a shorter merge); they are
+    doubled while the partials would not fit in ``ws_bytes``.  Items are issued longest first."""
+    tq_max = rows // g
+    groups = []  # (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b)
+    for b in range(len(qo_indptr) - 1):
+        qo_len = qo_indptr[b + 1] - qo_indptr[b]
+        npg = kv_indptr[b + 1] - kv_indptr[b]
+        kv_len = (npg - 1) * page_size + last_page_len[b] if npg > 0 else 0
+        for t0 in range(0, qo_len, tq_max):
+            tq = min(tq_max, qo_len - t0)
+            kv_end = min(kv_len, max(0, t0 + tq + kv_len - qo_len)) if causal else kv_len
+            for h in range(hkv):
+                groups.append((h, t0, tq, kv_end, kv_len, qo_len, qo_indptr[b], kv_indptr[b], b))
+    total = sum(gr[3] for gr in groups)
+    chunk = max(256, min(8192, -(-total // num_cus // 64) * 64 or 256))
+    while True:
+        items, merges, nslots = [], [], 0
+        for (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b) in groups:
+            nch = max(1, -(-kv_end // chunk))
+            if nch == 1:
+                items.append([b, h, t0, tq, 0, kv_end, -1, kv_len, qo_len, qo_start, kp0, 0])
+                continue
+            for c in range(nch):
+                items.append([b, h, t0, tq, c * chunk, min(kv_end, (c + 1) * chunk), nslots + c, kv_len,
+                              qo_len, qo_start, kp0, 0])
+            merges.append([nslots, nch, qo_start, t0, tq, h, 0, 0])
+            nslots += nch
+        a = lambda n: -(-n // 256) * 256
+        off_g = a(len(items) * 12 * 4)
+        off_ml = off_g + a(len(merges) * 8 * 4)
+        off_o = off_ml + a(nslots * rows * 8)
+        need = off_o + nslots * rows * head_dim * 4
+        if need <= ws_bytes or not merges or chunk >= 8192:
+            break
+        chunk = min(8192, chunk * 2)
+    if need > ws_bytes:
+        raise RuntimeError(f"prefill workspace too small: need {need} bytes")
+    items.sort(key=lambda it: it[4] - it[5])  # longest key range first
+    return {"items": items, "groups": merges, "chunk": chunk, "slots": nslots,
+            "off_groups": off_g, "off_ml": off_ml, "off_o": off_o, "bytes": need}
+
+
 class BatchPrefillWithPagedKVCacheWrapper:
     """Paged (chunked) prefill attention over ragged query rows (FlashInfer contract)."""
 
@@ -221,57 +271,18 @@ class BatchPrefillWithPagedKVCacheWrapper:
     _ROWS = 256
 
     def _schedule(self, dev: torch.device) -> None:
-        """The matrix-core kernel's work list.  Like FlashInfer's plan, this reads the (small)
-        indptr arrays back to the host once per batch.  Items are (request, KV head, 256/g query
-        tokens, chunk of the keys those tokens see); a long key range is cut into chunks so
-        that there is about one item per compute unit, and the chunks' partials are merged
-        by a second kernel.  Items are issued longest first."""
+        """The matrix-core kernel's work list (``prefill_work_list``) copied into the
+        workspace.  Like FlashInfer's plan, this reads the (small) indptr arrays back to the
+        host once per batch."""
         qo = self._qo_indptr.cpu().tolist()
         kp = self._indptr.cpu().tolist()
         last = self._last.cpu().tolist()
-        g = self._hq // self._hkv
-        tq_max = self._ROWS // g
-        groups = []  # (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b)
-        for b in range(self._batch):
-            qo_len = qo[b + 1] - qo[b]
-            npg = kp[b + 1] - kp[b]
-            kv_len = (npg - 1) * self._ps + last[b] if npg > 0 else 0
-            for t0 in range(0, qo_len, tq_max):
-                tq = min(tq_max, qo_len - t0)
-                kv_end = min(kv_len, max(0, t0 + tq + kv_len - qo_len)) if self._causal else kv_len
-                for h in range(self._hkv):
-                    groups.append((h, t0, tq, kv_end, kv_len, qo_len, qo[b], kp[b], b))
         self._nnz_q = qo[-1]
-        total = sum(gr[3] for gr in groups)
-        ncu = _num_cus(dev)
-
-        # chunks are whole steps of the kernel (64 keys), sized for about one item per CU:
-        # fewer, longer items split fewer key ranges (less partial traffic, a shorter merge)
-        chunk = max(256, min(8192, -(-total // ncu // 64) * 64 or 256))
         ws_bytes = self._workspace.numel() * self._workspace.element_size()
-        while True:
-            items, merges, nslots = [], [], 0
-            for (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b) in groups:
-                nch = max(1, -(-kv_end // chunk))
-                if nch == 1:
-                    items.append([b, h, t0, tq, 0, kv_end, -1, kv_len, qo_len, qo_start, kp0, 0])
-                    continue
-                for c in range(nch):
-                    items.append([b, h, t0, tq, c * chunk, min(kv_end, (c + 1) * chunk), nslots + c, kv_len,
-                                  qo_len, qo_start, kp0, 0])
-                merges.append([nslots, nch, qo_start, t0, tq, h, 0, 0])
-                nslots += nch
-            a = lambda n: -(-n // 256) * 256
-            off_g = a(len(items) * 12 * 4)
-            off_ml = off_g + a(len(merges) * 8 * 4)
-            off_o = off_ml + a(nslots * self._ROWS * 8)
-            need = off_o + nslots * self._ROWS * self._d * 4
-            if need <= ws_bytes or not merges or chunk >= 8192:
-                break
-            chunk = min(8192, chunk * 2)
-        if need > ws_bytes:
-            raise RuntimeError(f"prefill workspace too small: need {need} bytes")
-        items.sort(key=lambda it: it[4] - it[5])  # longest key range first
+        wl = prefill_work_list(qo, kp, last, self._hq // self._hkv, self._hkv, self._ps, self._causal, self._d,
+                               _num_cus(dev), ws_bytes, self._ROWS)
+        items, merges = wl["items"], wl["groups"]
+        off_g, off_ml, off_o = wl["off_groups"], wl["off_ml"], wl["off_o"]
         flat = [x for it in items for x in it] + [0] * ((off_g - len(items) * 48) // 4) + \
                [x for m in merges for x in m]
         if flat:
@@ -281,7 +292,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._n_items, self._n_groups = len(items), len(merges)
         self._items_ptr, self._groups_ptr = base, base + off_g
         self._ml_ptr, self._o_ptr = base + off_ml, base + off_o
-        self._chunk = chunk
+        self._chunk = wl["chunk"]
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,
             v_scale=None, out: torch.Tensor | None = None, lse=None, return_lse: bool = False,
