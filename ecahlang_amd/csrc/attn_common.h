@@ -30,13 +30,29 @@ struct DecodeParams {
   void* out;
   int64_t o_sn, o_sh;
   int32_t* counters;           // [B]
-  float2* part_ml;             // [num_ctas + B][hq] (running max, sum of exp)
+  float2* part_ml;             // [num_ctas + B][ml_stride] (running max, sum of exp)
   float* part_o;               // [num_ctas + B][hq][D], normalised partial output
   int32_t num_ctas;
   int32_t q_vec;               // q rows / strides allow 16-byte loads
   int32_t o_vec;               // out rows / strides allow 8-byte stores
   int32_t dynamic;             // matrix-core kernel: waves take pages on demand
+  int32_t ml_stride;           // float2 entries per part_ml slot: hq rounded up to a line
+  const int32_t* sched;        // matrix-core kernel: the plan's range records (decode_sched.h)
+  const int32_t* sched_hdr;    // ... and its global header
+  const int32_t* sched_head;   // ... and the dense heads of its ranges
+  int32_t r_cap;               // ranges the workspace holds
 };
+
+// A part_ml slot (one segment's (max, sum) pairs of every q head) spans whole 128-byte L2 lines,
+// so no line holds two slots.  The merger of a sequence reads its slots with plain loads; were a
+// line shared with another sequence's slot, that load could bring the other slot's line into
+// this XCD's L2 before its writer (on another XCD) stored it, and the other sequence's merger
+// on this XCD would then read the stale copy.
+constexpr int kLineBytes = 128;
+__host__ __device__ __forceinline__ int ml_slot_stride(int hq) {
+  constexpr int per = kLineBytes / 8;  // float2 entries per line
+  return (hq + per - 1) / per * per;
+}
 
 // Partition of the batch's `total` pages into n contiguous ranges (1 <= n <= total): the
 // first r = total % n ranges hold q + 1 pages, the others q = total / n.  32-bit arithmetic
@@ -137,13 +153,13 @@ struct MergeItem {
   // from clamped indices.
   __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int i, int nsw) {
     const int ns = nseg < kMergeRegs ? nseg : kMergeRegs;
-    const int64_t s0 = (int64_t)(list[i][1] + list[i][0]) * P.hq + h;
+    const int64_t slot0 = (int64_t)(list[i][1] + list[i][0]);
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
       if (s < nsw) {
-        const int64_t e = s0 + (int64_t)(s < ns ? s : ns - 1) * P.hq;
-        ml[s] = P.part_ml[e];
-        const float4* src = reinterpret_cast<const float4*>(P.part_o + e * D + d);
+        const int64_t slot = slot0 + (s < ns ? s : ns - 1);
+        ml[s] = P.part_ml[slot * P.ml_stride + h];
+        const float4* src = reinterpret_cast<const float4*>(P.part_o + (slot * P.hq + h) * D + d);
         po[s][0] = src[0];
         po[s][1] = src[1];
       } else {  // (never selected by finish: set so that no value is left undefined)
@@ -152,25 +168,32 @@ struct MergeItem {
       }
     }
   }
-  __device__ __forceinline__ void finish(const DecodeParams& P) const {
+  // Fold of the first nsw (wave-uniform, >= this item's capped segment count) loaded segments.
+  // The fold is vector-ALU work repeated by every thread of the merging workgroup, so it runs
+  // only over the wave's own segment count and uses v_exp_f32 (arguments <= 0) directly.
+  __device__ __forceinline__ void finish(const DecodeParams& P, int nsw) const {
     if (b < 0) return;
     float M = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < kMergeRegs; ++s) M = s < nseg ? fmaxf(M, ml[s].x) : M;
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s >= nsw) break;
+      M = s < nseg ? fmaxf(M, ml[s].x) : M;
+    }
+    const float mu = M == -INFINITY ? 0.f : M;
     float den = 0.f;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
-      const float c = (s < nseg && ml[s].y > 0.f) ? exp2f(ml[s].x - M) * ml[s].y : 0.f;
+      if (s >= nsw) break;
+      const float c = (s < nseg && ml[s].y > 0.f) ? __builtin_amdgcn_exp2f(ml[s].x - mu) * ml[s].y : 0.f;
       den += c;
-      // Selects, not a branch: a dropped segment's row may hold anything (0 * NaN), and a
-      // value used only under a branch lets the compiler sink its load into that branch,
-      // where it is issued late and waited for at once.
-      const bool use = c != 0.f;
+      // Partial rows are finite (normalised averages of finite value rows; a segment whose
+      // tokens were all masked stores zeros), and loads past this item's segment count repeat a
+      // real segment, so c * row needs no select.
       const float v[8] = {po[s][0].x, po[s][0].y, po[s][0].z, po[s][0].w,
                           po[s][1].x, po[s][1].y, po[s][1].z, po[s][1].w};
 #pragma unroll
-      for (int x = 0; x < 8; ++x) acc[x] += use ? c * v[x] : 0.f;
+      for (int x = 0; x < 8; ++x) acc[x] = __builtin_fmaf(c, v[x], acc[x]);
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
     T* orow = reinterpret_cast<T*>(P.out) + b * P.o_sn + h * P.o_sh + d;
@@ -202,9 +225,10 @@ __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*
     int nsw = a.nseg < kMergeRegs ? a.nseg : kMergeRegs;  // the wave's longest item
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) nsw = max(nsw, __shfl_xor(nsw, off, 64));
-    a.load(P, list, i, __builtin_amdgcn_readfirstlane(nsw));
+    nsw = __builtin_amdgcn_readfirstlane(nsw);
+    a.load(P, list, i, nsw);
     asm volatile("" ::: "memory");  // every load is issued before the fold
-    a.finish(P);
+    a.finish(P, nsw);
   };
   // The first round (all of it when nitems <= blockDim.x, the usual case) is peeled off the
   // loop: inside a loop, registers that the previous round's loads filled can make the
@@ -223,18 +247,18 @@ template <typename T, int D>
 __device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi) {
   T* out = reinterpret_cast<T*>(P.out);
   const int nseg = w_hi - w_lo + 1;
-  const int64_t s0 = (int64_t)(w_lo + b) * P.hq;
+  const int64_t slot0 = (int64_t)(w_lo + b);
   for (int idx = threadIdx.x; idx < P.hq * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
-    const float2* ml = P.part_ml + s0 + h;
-    const float* po = P.part_o + (s0 + h) * D + d;
+    const float2* ml = P.part_ml + slot0 * P.ml_stride + h;
+    const float* po = P.part_o + (slot0 * P.hq + h) * D + d;
     float M = -INFINITY;
 #pragma unroll 4
-    for (int s = 0; s < nseg; ++s) M = fmaxf(M, ml[(int64_t)s * P.hq].x);
+    for (int s = 0; s < nseg; ++s) M = fmaxf(M, ml[(int64_t)s * P.ml_stride].x);
     float num = 0.f, den = 0.f;
 #pragma unroll 4
     for (int s = 0; s < nseg; ++s) {
-      const float2 v = ml[(int64_t)s * P.hq];
+      const float2 v = ml[(int64_t)s * P.ml_stride];
       const float o = po[(int64_t)s * P.hq * D];
       const float c = v.y > 0.f ? exp2f(v.x - M) * v.y : 0.f;
       num += c * o;
@@ -244,11 +268,11 @@ __device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int
   }
 }
 
-// Partial state of one (slot, q head): normalised output and (max, sum) in base-2 units.
-__device__ __forceinline__ void store_partial_ml(const DecodeParams& P, int64_t sidx, float m, float l) {
-  float* ml = reinterpret_cast<float*>(P.part_ml);
-  st_dev(ml + 2 * sidx, m);
-  st_dev(ml + 2 * sidx + 1, l);
+// (max, sum) in base-2 units of one (slot, q head) of a split segment.
+__device__ __forceinline__ void store_partial_ml(const DecodeParams& P, int64_t slot, int hq, float m, float l) {
+  float* ml = reinterpret_cast<float*>(P.part_ml + slot * P.ml_stride + hq);
+  st_dev(ml, m);
+  st_dev(ml + 1, l);
 }
 
 // Arrival protocol after a workgroup wrote its partial for sequence b.  Returns true in
@@ -285,30 +309,6 @@ __device__ __forceinline__ void zero_empty_sequences(const DecodeParams& P) {
 // and the workgroups touching a sequence are exactly Ranges::owner(first)..owner(last).
 __device__ __forceinline__ int effective_ranges(int num_ctas, int total) {
   return num_ctas < total ? num_ctas : total;
-}
-
-// The matrix-core kernel also caps a range at kPidCap pages (its page ids are staged in
-// LDS), using ceil(total / kPidCap) ranges when that exceeds the workgroup count.
-constexpr int kPidCap = 2048;
-__host__ __device__ __forceinline__ int64_t decode_ranges_max(int num_ctas, int64_t total) {
-  int64_t need = (total + kPidCap - 1) / kPidCap;
-  return need > num_ctas ? need : num_ctas;
-}
-__device__ __forceinline__ int decode_ranges(int num_ctas, int total) {
-  const int n = total < num_ctas ? total : num_ctas;
-  const int need = (int)(((unsigned)total + kPidCap - 1) / kPidCap);
-  return n > need ? n : need;
-}
-
-// Largest b in [0, n) with a[b] <= x over an LDS copy of indptr (a[0] <= x assumed);
-// the result is wave-uniform.
-__device__ __forceinline__ int lds_upper_index(const int* a, int n, int64_t x) {
-  int lo = 0, hi = n;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if ((int64_t)a[mid] <= x) lo = mid; else hi = mid;
-  }
-  return __builtin_amdgcn_readfirstlane(lo);
 }
 
 // Largest b in [0, B) with indptr[b] <= p, found by the whole wave: each lane loads one

@@ -1,30 +1,50 @@
 // Batch paged decode: C-ABI entry points, workspace layout and kernel choice.
 //
-//   pkv_decode_workspace_bytes / pkv_decode_workspace_init  <- BatchDecodeWithPagedKVCacheWrapper.plan
-//   pkv_batch_decode                                        <- BatchDecodeWithPagedKVCacheWrapper.run
+//   pkv_decode_workspace_bytes / pkv_decode_workspace_init / pkv_decode_plan
+//                                          <- BatchDecodeWithPagedKVCacheWrapper.plan
+//   pkv_batch_decode                       <- BatchDecodeWithPagedKVCacheWrapper.run
 //   (ecahlang/main.py:203-204 construct, :341-347 / :444-455 plan, :68 run)
 //
-// Workspace (caller-owned bytes, 256-byte aligned regions):
-//   [counters: int32 x batch] [part_ml: float2 x (ctas+batch) x Hq] [part_o: f32 x (ctas+batch) x Hq x D]
+// Workspace (caller-owned bytes, 256-byte aligned regions; R = decode_ranges_cap ranges):
+//   [counters: int32 x batch] [part_ml: float2 x (R+batch) x ml_slot_stride(Hq)]
+//   [part_o: f32 x (R+batch) x Hq x D]  (each part_ml slot is whole 128-byte lines)
+//   [schedule: global header + empty list (kGlobHdr + batch int32), R heads of kHeadWords
+//    int32, R records of kRecStride int32, plan scratch rank[batch], first-sequence[R] and range starts[R + 1]]
 #include "attn_common.h"
+#include "decode_sched.h"
 #include "../../include/pagedkv.h"
 
 using namespace pkv;
+
+namespace pkv {
+int decode_plan_launch(const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+                       const int32_t* last, int batch, int num_ctas, int page_size, int seg_cost,
+                       int r_cap, int32_t* ghdr, int32_t* recs, int32_t* heads, int32_t* rank,
+                       int32_t* bf, int32_t* starts, hipStream_t s);
+}
 
 namespace {
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t cnt, ml, o, total;
+  size_t cnt, ml, o, ghdr, heads, recs, rank, bf, starts, total;
+  int64_t rcap;
 };
-inline WsLayout ws_layout(int batch, int hq, int d, int ctas) {
+inline WsLayout ws_layout(int batch, int hq, int d, int ctas, int64_t num_indices) {
   WsLayout L;
-  size_t segs = (size_t)ctas + batch;
+  L.rcap = decode_ranges_cap(ctas, num_indices);
+  size_t segs = (size_t)L.rcap + batch;
   L.cnt = 0;
   L.ml = align256(sizeof(int32_t) * (size_t)batch);
-  L.o = L.ml + align256(sizeof(float) * 2 * segs * hq);
-  L.total = L.o + align256(sizeof(float) * segs * hq * d);
+  L.o = L.ml + align256(sizeof(float) * 2 * segs * ml_slot_stride(hq));
+  L.ghdr = L.o + align256(sizeof(float) * segs * hq * d);
+  L.heads = L.ghdr + align256(sizeof(int32_t) * ((size_t)kGlobHdr + batch));
+  L.recs = L.heads + align256(sizeof(int32_t) * (size_t)L.rcap * kHeadWords);
+  L.rank = L.recs + align256(sizeof(int32_t) * (size_t)L.rcap * kRecStride);
+  L.bf = L.rank + align256(sizeof(int32_t) * (size_t)batch);
+  L.starts = L.bf + align256(sizeof(int32_t) * (size_t)L.rcap);
+  L.total = L.starts + align256(sizeof(int32_t) * ((size_t)L.rcap + 1));
   return L;
 }
 
@@ -32,15 +52,18 @@ __global__ void zero_i32_kernel(int32_t* p, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 
+bool ws_args_ok(int32_t batch, int32_t hq, int32_t d, int32_t ctas, int64_t num_indices) {
+  return batch >= 0 && hq > 0 && d > 0 && ctas > 0 && num_indices >= 0 &&
+         decode_ranges_cap(ctas, num_indices) + batch < (1 << 30);
+}
+
 }  // namespace
 
 extern "C" int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads,
                                               int32_t head_dim, int32_t num_ctas,
                                               int64_t num_indices) {
-  if (batch < 0 || num_qo_heads <= 0 || head_dim <= 0 || num_ctas <= 0 || num_indices < 0)
-    return kBadArg;
-  const int64_t ranges = decode_ranges_max(num_ctas, num_indices);
-  return (int64_t)ws_layout(batch, num_qo_heads, head_dim, (int)ranges).total;
+  if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
+  return (int64_t)ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices).total;
 }
 
 extern "C" int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream) {
@@ -49,6 +72,24 @@ extern "C" int pkv_decode_workspace_init(void* workspace, int32_t batch, void* s
   hipLaunchKernelGGL(zero_i32_kernel, dim3((batch + 255) / 256), dim3(256), 0, (hipStream_t)stream,
                      (int32_t*)workspace, batch);
   return (int)hipGetLastError();
+}
+
+extern "C" int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indices,
+                               int64_t num_indices, const int32_t* kv_last_page_len, int32_t batch,
+                               int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t page_size, int32_t num_ctas, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  if (batch <= 0) return kOk;
+  if (page_size <= 0) return kBadPageSize;
+  if (num_kv_heads <= 0) return kBadArg;
+  if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
+  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices);
+  if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
+  char* ws = (char*)workspace;
+  return decode_plan_launch(kv_indptr, kv_indices, num_indices, kv_last_page_len, batch, num_ctas,
+                            page_size, seg_cost_pages(num_kv_heads, head_dim, page_size), (int)L.rcap, (int32_t*)(ws + L.ghdr), (int32_t*)(ws + L.recs), (int32_t*)(ws + L.heads),
+                            (int32_t*)(ws + L.rank), (int32_t*)(ws + L.bf), (int32_t*)(ws + L.starts),
+                            (hipStream_t)stream);
 }
 
 extern "C" int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
@@ -73,8 +114,8 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   if (page_size <= 0) return kBadPageSize;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return kBadHeadDim;
   if (num_indices < 0 || num_pages < 0) return kBadArg;
-  // Partial slots are indexed by range + sequence; ranges never exceed this bound.
-  WsLayout L = ws_layout(batch, num_qo_heads, head_dim, (int)decode_ranges_max(num_ctas, num_indices));
+  if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
+  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices);
   if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
   DecodeParams P;
   P.q = q; P.q_sn = q_stride_n; P.q_sh = q_stride_h;
@@ -88,14 +129,21 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   P.counters = (int32_t*)(ws + L.cnt);
   P.part_ml = (float2*)(ws + L.ml);
   P.part_o = (float*)(ws + L.o);
+  P.ml_stride = ml_slot_stride(num_qo_heads);
+  P.sched_hdr = (const int32_t*)(ws + L.ghdr);
+  P.sched = (const int32_t*)(ws + L.recs);
+  P.sched_head = (const int32_t*)(ws + L.heads);
+  P.r_cap = (int32_t)L.rcap;
   P.num_ctas = num_ctas;
   P.dynamic = (flags & PKV_DECODE_DYNAMIC) != 0;
   const int es = dtype == kF32 ? 4 : 2;
   P.q_vec = ((uintptr_t)q % 16 == 0) && ((q_stride_n * es) % 16 == 0) && ((q_stride_h * es) % 16 == 0);
   P.o_vec = ((uintptr_t)out % 8 == 0) && ((o_stride_n * es) % 8 == 0) && ((o_stride_h * es) % 8 == 0);
   hipStream_t s = (hipStream_t)stream;
-  int g = num_qo_heads / num_kv_heads;
-  if (!(flags & PKV_DECODE_VALU) && decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
+  const int g = num_qo_heads / num_kv_heads;
+  // The matrix-core kernel reads the schedule pkv_decode_plan wrote into this workspace.
+  if ((flags & PKV_DECODE_PLANNED) && !(flags & PKV_DECODE_VALU) && P.q_vec && page_size == 16 &&
+      decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
     return decode_mfma_dispatch(P, dtype, head_dim, s);
   return decode_valu_dispatch(P, dtype, head_dim, s);
 }

@@ -1,29 +1,34 @@
 // Paged decode on the matrix cores (fp16 / bf16 caches, page_size 16, head_dim 64 or 128,
-// GQA group <= 16).  Same contract as the vector kernel (FlashInfer
-// BatchDecodeWithPagedKVCacheWrapper.run, ecahlang/main.py:68); same page-range partition
-// and split merge (attn_common.h).
+// GQA group <= 16), driven by the plan's schedule (decode_sched.h).  Same contract as the
+// vector kernel (FlashInfer BatchDecodeWithPagedKVCacheWrapper.run, ecahlang/main.py:68).
 //
-// Why matrix cores in decode: with a GQA group of g query heads per KV head every K/V byte
-// feeds g multiply-adds in Q.K^T and g more in P.V.  At g = 8 (Qwen2.5-3B) that is 4 MACs per
-// cache byte, which on the vector ALUs (64 fp32 FMA/clk/CU) costs about as many cycles as
-// streaming the byte from HBM; on the matrix cores it is ~10% of that, leaving the kernel
-// bound by HBM alone.  The g query heads of one KV head form the 16 MFMA columns (g < 16
-// leaves columns idle; compute is not the bound).
+// Work unit: one page of one head block, i.e. 16 tokens x HB KV heads, where HB is the largest
+// power of two with HB * g <= 16 query heads (the MFMA's 16 columns), HB * head_dim <= 256 and
+// HB | Hkv.  At Qwen2.5-3B (Hkv 2, g 8, D 128) a unit is a whole page, both heads: 8 KB of K
+// and 8 KB of V, each a contiguous run of 16 token rows of 512 bytes.  A wave copies a unit
+// global -> LDS with non-temporal global_load_lds_dwordx4 (each instruction reads 1 KB of whole
+// 128-byte lines), which streams measurably faster than per-head 64-byte row pieces into
+// registers, and needs no registers for the data in flight.
 //
-// Per wave, per page (16 tokens of one KV head):
-//   S[t][n]  = sum_d K[t][d] Q[n][d]    v_mfma_f32_16x16x32: A = K rows straight from HBM
-//                                       (lane = token l%16, 8 dims), B = Q (lane = head l%16)
-//   online softmax on S in the accumulator layout (lane holds 4 tokens of one head)
-//   O^T[d][n] += sum_t V[t][d] P[t][n]  v_mfma_f32_16x16x16: B = P exactly as the softmax
-//                                       left it; A = V^T, read from an XOR-swizzled LDS
-//                                       copy of the page (coalesced 16-byte HBM loads)
-// The reduction index of both products only has to agree between the two operands, so the
-// dim order inside K and Q operands is chosen to make each K load 64 contiguous bytes.
-// Waves of one workgroup split the pages of each segment; their states meet in LDS at the
-// segment's end, where every wave folds the copies of the output tiles it owns and writes
-// them (as output rows, or as the partial of a sequence split across workgroups).
+// Per unit (column n = query head hb*HB*g + n of the block, n < HB*g):
+//   S[t][n]   = sum over the unit row r of K[t][r] * Qbd[r][n]    v_mfma_f32_16x16x32, A = K
+//               rows from LDS, B = Qbd, block-diagonal: Q of column n in the dims of its own KV
+//               head, zero in the other heads' dims, so one tile holds every head's scores
+//   online softmax per column in the accumulator layout (lane: column l%16, tokens 4*(l/16)+i)
+//   O^T[d][n] += sum_hh sum_t V_hh[t][d] * P[t][n] [head(n) == hh]   v_mfma_f32_16x16x32 over
+//               two heads at once (reduction slots 0-3 = head 2u, 4-7 = head 2u+1; A = two
+//               ds_read_b64_tr_b16 of the staged V, B = P masked to each head's columns)
+// Every output column is a distinct query head, so the accumulators hold D x 16 values.
+//
+// A workgroup (8 waves) owns ranges of the schedule; the J = 8 / (Hkv / HB) waves of a head
+// block split the range's pages (wave j takes pages j, j+J, ...: a fixed order, so the result is
+// reproducible).  Each wave keeps one unit in flight: the next unit's K is requested as soon as
+// the current K is consumed, its V as soon as the current V is.  At a segment (sequence) end the
+// J states meet in LDS; the owner of each 16-dim tile writes it: output rows, or the partial of a
+// sequence split across ranges, merged by the last workgroup to finish (attn_common.h).
 #include "attn_common.h"
 #include "mfma_common.h"
+#include "decode_sched.h"
 #include "../../include/pagedkv.h"
 
 using namespace pkv;
@@ -32,211 +37,160 @@ namespace {
 
 using namespace pkv::mfma;
 
-// Dynamic LDS of the kernel, in bytes (host and device compute the same layout):
-//   tiles  one V page per wave, XOR-swizzled                        W * 16 * D * 2
-//   slots  softmax states met at a segment end: (max, sum) of every
-//          wave, and each output tile of a head from the J - 1 waves
-//          that do not own it                                        W * 512 + hkv * (J - 1) * MT * 1024
-//   meta   indptr[0..B] and last_page_len[0..B) (B <= kMetaCap)
-//   q      query rows of the range's first qseg sequences, plus one slot filled on demand
-//          for a range with more segments
-constexpr int kMetaCap = 2048;    // batch limit: page-table rows are staged in LDS
-constexpr int kMaxSplit = 32;     // split segments whose arrival a workgroup defers
-constexpr int kQSegMax = 4;
+constexpr int W = 8;                // waves per workgroup
+constexpr int NT = W * 64;
+constexpr int kQArea = 8192;        // LDS bytes for query rows of the range's first segments
+constexpr int kSegLds = 64;         // segment records staged in LDS (more are read from memory)
+constexpr int kMaxSplit = 32;       // split segments whose arrival a workgroup defers
+constexpr float kLazyMax = 8.f;     // a column's reference max moves only on jumps > 2^8
 
-__host__ __device__ constexpr int align_up(int x, int a) { return (x + a - 1) / a * a; }
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-struct MfmaLds {
-  int tiles, slots, copies, meta, q, total;
+// One wave-wide copy global -> LDS: lane l's 16 bytes at src (per lane) land at LDS byte
+// dst + 16 l (dst wave-uniform, in M0).  Inline assembly, so the compiler neither tracks nor
+// waits for it: the kernel orders these copies with explicit vmcnt waits.  `nt` streams the
+// K/V pages past the caches; small metadata copies use the default policy.
+__device__ __forceinline__ void dma16_nt(const void* src, const char* dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0) : "memory");
+}
+__device__ __forceinline__ void dma16(const void* src, const char* dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+
+// XOR swizzles of 16-byte chunk positions inside a staged row of RB bytes (the low four bits
+// only, so a row's chunks stay in their own 256-byte half and every copy still reads whole
+// lines).  K rows are read as the QK A operand (16 rows, one chunk per 16-lane group): distinct
+// bank groups for the 16 rows.  V rows are read by ds_read_b64_tr_b16 (per 32 lanes, 8 rows x 2
+// adjacent chunks): distinct bank groups for those 16 chunks.
+template <int RB>
+__device__ __forceinline__ int kx(int t) {
+  return RB >= 256 ? (t & 15) : ((t >> 1) & 7);
+}
+template <int RB>
+__device__ __forceinline__ int vx(int t) {
+  return RB >= 256 ? 2 * (t & 7) : 2 * ((t >> 1) & 3);
+}
+
+// Sum of the J (<= W) copies of a tile, read four at a time with every read of a batch issued
+// before any add (copies past J repeat copy 0 and are dropped).
+template <typename F>
+__device__ __forceinline__ f4 fold_copies(int J, F&& copy) {
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b0 = 0; b0 < W; b0 += 4) {
+    if (b0 >= J) break;
+    f4 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = copy(b0 + k < J ? b0 + k : 0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc += b0 + k < J ? x[k] : f4{0.f, 0.f, 0.f, 0.f};
+  }
+  return acc;
+}
+
+struct Seg {
+  int b, beg, end, nv, wlo, whi;
 };
-template <int D, int W>
-__host__ __device__ inline MfmaLds mfma_lds(int hkv, int hq, int qseg) {
-  constexpr int MT = D / 16;
-  const int J = W / hkv;
-  MfmaLds L;
-  L.tiles = 0;
-  L.slots = W * 16 * D * 2;                 // (max, sum) pairs: W * 64 float2
-  L.copies = L.slots + W * 64 * 8;          // tile copies: [hkv][MT][J - 1][64] float4
-  L.meta = align_up(L.copies + hkv * (J - 1) * MT * 1024, 16);
-  L.q = L.meta + align_up((2 * kMetaCap + 1) * 4, 16);
-  L.total = L.q + (qseg + 1) * hq * D * 2;
-  return L;
-}
-// Query rows staged per range: as many sequences as fit in 32 KB, between 1 and kQSegMax.
-__host__ __device__ inline int mfma_qseg(int hq, int d) {
-  int n = 32768 / (hq * d * 2);
-  return n < 1 ? 1 : (n > kQSegMax ? kQSegMax : n);
+__device__ __forceinline__ Seg unpack_seg(int4 v, int len, int batch) {
+  Seg s;
+  s.b = v.x < 0 ? 0 : (v.x >= batch ? batch - 1 : v.x);
+  s.beg = v.y & 0xFFFF;
+  s.end = (v.y >> 16) & 0xFFFF;
+  s.end = s.end > len ? len : s.end;
+  s.beg = s.beg > s.end ? s.end : s.beg;
+  s.nv = v.z < 0 ? 0 : (v.z > 16 ? 16 : v.z);
+  s.wlo = v.w & 0xFFFF;
+  s.whi = (v.w >> 16) & 0xFFFF;
+  return s;
 }
 
-// J = W / hkv waves share each KV head (a template parameter: the combine's loops and
-// register arrays are sized by it).
-template <typename T, int D, int W, int J>
-__global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
-  constexpr int NT = W * 64;
-  constexpr int KSTEPS = D / 32;        // Q.K^T matrix steps (k = 32 dims each)
-  constexpr int MT = D / 16;            // P.V output tiles of 16 dims
-  constexpr int CPR = D / 8;            // 16-byte chunks per token row
-  constexpr int VCH = 16 * CPR / 64;    // V chunks per lane per page
-  constexpr int ROWB = D * 2;           // bytes per staged V row
-  constexpr int TILEB = 16 * ROWB;      // bytes per staged V page
+template <int HB, int D>
+struct Shape {
+  static constexpr int RW = HB * D;        // elements of a unit row
+  static constexpr int RB = RW * 2;        // bytes of a unit row
+  static constexpr int CPR = RB / 16;      // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;     // rows per 1 KB copy
+  static constexpr int NI = 16 / RPI;      // copies per K (or V) tile
+  static constexpr int TILE = 16 * RB;     // bytes of a K (or V) tile
+  static constexpr int KS = RW / 32;       // QK steps
+  static constexpr int KSH = D / 32;       // QK steps per head
+  static constexpr int MT = D / 16;        // output tiles of 16 dims
+  static constexpr int LDS = W * 2 * TILE + kQArea;  // dynamic LDS
+};
 
-  extern __shared__ __align__(16) char smem[];
-  __shared__ int s_pid[kPidCap];
-  __shared__ int s_split[kMaxSplit][3];  // deferred arrivals: sequence, w_lo, w_hi
-  __shared__ int s_merge[kMaxSplit][3];  // merges owed after the arrivals
+template <typename T, int D, int HB>
+__global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
+  using S = Shape<HB, D>;
+  constexpr int RB = S::RB, CPR = S::CPR, RPI = S::RPI, NI = S::NI, TILE = S::TILE;
+  constexpr int KS = S::KS, KSH = S::KSH, MT = S::MT;
+
+  extern __shared__ __align__(16) char smem[];  // [W][K tile, V tile] | query rows
+  __shared__ int s_pid[kRangePages];
+  __shared__ int4 s_seg[kSegLds];
+  __shared__ float2 s_ml[W][16];
+  __shared__ f4 s_x[2][W][64];                // tile exchange at interior segment ends
+  __shared__ int s_split[kMaxSplit][3];       // deferred arrivals: sequence, w_lo, w_hi
+  __shared__ int s_merge[kMaxSplit][3];       // merges owed after the arrivals
   __shared__ int s_nmerge;
-  __shared__ int s_next[8];              // per KV head: next range page to hand out
-  __shared__ int s_bf, s_bl, s_nseg;     // the range's first / last sequence, segment count
-  // readfirstlane: the wave index (and all derived from it) is wave-uniform, so page ids
-  // and addresses that depend on it become scalar values.
+  __shared__ int s_next[W];                   // PKV_DECODE_DYNAMIC: next page per head block
+
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int lr = lane & 15, lg = lane >> 4;
-
-  const int B = P.batch, hkv = P.hkv, g = P.hq / hkv;
-  const int qseg = mfma_qseg(P.hq, D);
-  const MfmaLds L = mfma_lds<D, W>(hkv, P.hq, qseg);
-  char* vtile = smem + L.tiles + wave * TILEB;
-  float2* s_ml = reinterpret_cast<float2*>(smem + L.slots);   // [W][64]
-  f4* s_copy = reinterpret_cast<f4*>(smem + L.copies);        // [hkv][MT][J - 1][64]
-  int* s_indptr = reinterpret_cast<int*>(smem + L.meta);      // [kMetaCap + 1]
-  int* s_lastlen = s_indptr + kMetaCap + 1;                   // [kMetaCap]
-  const T* s_q = reinterpret_cast<const T*>(smem + L.q);      // [qseg + 1][hq][D]
-  T* s_qw = reinterpret_cast<T*>(smem + L.q);
-
-  // Heads are dealt round-robin (h = wave % hkv): waves of one SIMD differ in issue
-  // priority by age, and this gives every head the same mix of older and younger waves.
-  const int h = wave % hkv, j = wave / hkv;  // this wave's KV head and its rank among the J
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int B = P.batch, g = P.hq / P.hkv;
+  const int NHB = P.hkv / HB, J = W / NHB;
+  const int hb = wave % NHB, j = wave / NHB;
   const bool active = j < J;
-
-  const int N0 = P.num_ctas;
-  // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each
-  // XCD a run of consecutive ranges keeps a split sequence's partials on one L2.
-  const int w0 = (N0 % 8 == 0) ? (int)(blockIdx.x % 8) * (N0 / 8) + (int)(blockIdx.x / 8)
-                               : (int)blockIdx.x;
-  // The first range's page ids are requested together with round 1, assuming the page list
-  // holds exactly indptr[B] entries (kv_indices sized to the batch): the partition then
-  // depends on num_indices alone.  Round 1 confirms the guess, or they are read again.
-  static_assert(kPidCap <= 4 * NT, "four page ids per thread");
-  const int tg = (int)(P.num_indices < INT_MAX ? P.num_indices : INT_MAX);
-  int pv[4];
-  int gp0 = 0, glen = 1, ng = 0;
-  {
-    if (tg > 0) {
-      ng = decode_ranges(N0, tg);
-      if (w0 < ng) {
-        const Ranges rg(ng, tg);
-        gp0 = rg.start(w0);
-        glen = rg.start(w0 + 1) - gp0;
-      }
-    }
-    const int32_t* src = tg > 0 ? P.indices + gp0 : P.indptr;  // (a valid address either way)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {  // unconditional loads from clamped indices
-      const int t = threadIdx.x + r * NT;
-      pv[r] = src[tg > 0 ? (t < glen ? t : glen - 1) : 0];
-    }
-  }
-
-  // ---- round 1: the page table's row pointers and last-page lengths into LDS
-  // (B <= kMetaCap <= 4 * NT).  The loads are unconditional, from clamped indices, and all
-  // are issued before the first LDS write: a load under a divergent branch gets a wait for
-  // its result at the branch's end, which would serialise them.
-  {
-    static_assert(kMetaCap <= 4 * NT, "four rows per thread");
-    int iv[5], lv[4];
-#pragma unroll
-    for (int r = 0; r < 5; ++r) {
-      const int i = threadIdx.x + r * NT;
-      iv[r] = P.indptr[i < B ? i : B];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = threadIdx.x + r * NT;
-      lv[r] = P.last[i < B - 1 ? i : B - 1];
-    }
-#pragma unroll
-    for (int r = 0; r < 5; ++r) {
-      const int i = threadIdx.x + r * NT;
-      if (i <= B) s_indptr[i] = iv[r];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = threadIdx.x + r * NT;
-      if (i < B) s_lastlen[i] = lv[r];
-    }
-  }
-  if (threadIdx.x == 0) {
-    s_nseg = 0;
-    s_bf = INT_MAX;
-    s_bl = -1;
-  }
-  if (tg > 0 && w0 < ng) {  // the first range's page ids, as the speculative read gave them
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {  // ids outside the pool are read as absent (-1)
-      const int t = threadIdx.x + r * NT;
-      if (t < glen) s_pid[t] = ((int64_t)pv[r] >= 0 && (int64_t)pv[r] < P.num_pages) ? pv[r] : -1;
-    }
-  }
-  if (blockIdx.x == 0) zero_empty_sequences<T, D>(P);
-  lds_barrier();
-  auto rd = [&](const int* lds_arr, int i) __attribute__((always_inline)) -> int {  // uniform LDS read
-    return __builtin_amdgcn_readfirstlane(lds_arr[i]);
-  };
-  int total = rd(s_indptr, B);
-  total = (int64_t)total < P.num_indices ? total : (int)P.num_indices;
-  if (total <= 0) return;
-  // Ranges: one per workgroup, never more than there are pages and never more than
-  // kPidCap pages each (a workgroup then walks ranges w, w + N0, ...).
-  const int N = decode_ranges(N0, total);
-  const Ranges R(N, total);
+  char* kbuf = smem + wave * 2 * TILE;
+  char* vbuf = kbuf + TILE;
+  char* qarea = smem + W * 2 * TILE;
+  const int qrow = P.hq * D * 2;                       // bytes of one sequence's query rows
+  const int qcap = min(4, kQArea / qrow);              // sequences whose rows are staged
+  const int ncol = HB * g;                             // columns in use
+  const int hn = lr / g;                               // KV head (in the block) of my column
+  const bool colv = active && lr < ncol;
+  const int qh = hb * ncol + (colv ? lr : 0);          // query head of my column
 
   const T* kc = reinterpret_cast<const T*>(P.k_cache);
   const T* vc = reinterpret_cast<const T*>(P.v_cache);
   const T* qall = reinterpret_cast<const T*>(P.q);
   T* out = reinterpret_cast<T*>(P.out);
-  const int64_t rowstride = (int64_t)hkv * D;  // elements between tokens in a page
-  const int64_t hoff = (int64_t)(active ? h : 0) * D;
-  // Per-lane element offsets inside a page: K in the Q.K^T operand layout (token lr,
-  // dims 8*lg + 32*s), V in plain 16-byte row chunks.
-  const uint32_t koff = (uint32_t)(lr * rowstride + 8 * lg);
-  uint32_t voff[VCH];
-#pragma unroll
-  for (int r = 0; r < VCH; ++r) {
-    const int c = lane + 64 * r;
-    voff[r] = (uint32_t)((c / CPR) * rowstride + 8 * (c % CPR));
-  }
+  const int64_t rowstride = (int64_t)P.hkv * D;        // elements between token rows
+  const int64_t hboff = (int64_t)hb * HB * D;
 
-  // A page id outside the pool is read as page 0; its tokens are masked (nv = 0).  Past the
-  // range's end the last page is loaded again (an L2 hit, never used), so the load after a
-  // wave's last page is still a valid one.
-  auto load_page = [&](int pgid, uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH]) __attribute__((always_inline)) {
-    const int pg = pgid < 0 ? 0 : pgid;
-    const T* kb = kc + (int64_t)pg * P.page_stride + hoff;  // uniform base
-    const T* vb = vc + (int64_t)pg * P.page_stride + hoff;
+  // copy of unit (page pg) rows into a staged tile; `x` is the row swizzle
+  auto issue_tile = [&](const T* base, int64_t pg, char* dst, bool isv) __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-      kr[s] = *reinterpret_cast<const uint4*>(kb + koff + 32 * s);
-#pragma unroll
-    for (int r = 0; r < VCH; ++r) vr[r] = *reinterpret_cast<const uint4*>(vb + voff[r]);
+    for (int i = 0; i < NI; ++i) {
+      const int t = i * RPI + lane / CPR, pos = lane % CPR;
+      const int col = pos ^ (isv ? vx<RB>(t) : kx<RB>(t));
+      dma16_nt(base + pg * P.page_stride + t * rowstride + hboff + 8 * col, dst + i * 1024);
+    }
+  };
+  auto page_ok = [&](int pid) __attribute__((always_inline)) -> bool {
+    return pid >= 0 && (int64_t)pid < P.num_pages;
   };
 
-  // One page buffer per wave: a wave has one page in flight.  With the eight waves of every
-  // CU each holding one (~16 MB in flight over the chip, more than the HBM's bandwidth-delay
-  // product), this is faster than two per wave: 40.9 against 42.1 us per launch at the
-  // Qwen2.5-3B B=64 batch, and the wave needs 221 registers instead of 254.
-  uint4 kA[KSTEPS], vA[VCH];
-
-  // Deferred arrivals (split segments recorded in s_split; the count is kept in a register
-  // in every wave, as whether a segment is split is the same in all of them): every wave
-  // waits for its own partial stores, then one lane per split bumps that sequence's counter
-  // (all in parallel); the splits that arrived last are compacted into s_merge and merged
-  // by the whole workgroup at once.  Inside the page loop (a full record) the register-light
-  // global-memory merge is used: the page buffers are live there.
+  const int N0 = P.num_ctas;
+  // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each XCD a
+  // run of consecutive ranges keeps a split sequence's partials mostly on one L2.
+  const int w0 = (N0 % 8 == 0) ? (int)(blockIdx.x % 8) * (N0 / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
   int nsplit = 0;
+
+  // Deferred arrivals of split segments: every wave waits for its own partial stores, then one
+  // lane per split bumps that sequence's counter (all in parallel); the splits that arrived last
+  // are merged by the whole workgroup at once.  Inside the page loop (a full record) the
+  // register-light global-memory merge is used.
   auto flush_splits = [&](bool in_loop) __attribute__((always_inline)) {
-    wait_stores();  // this wave's partial stores are complete (device-visible)
-    lds_barrier();  // ... in every wave; the split records are visible
+    wait_stores();
+    lds_barrier();
     if (wave == 0) {
       int sb = 0, lo = 0, hi = 0, last = 0;
       if (lane < nsplit) {
@@ -245,7 +199,6 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
         hi = s_split[lane][2];
         const int old = atomicAdd(&P.counters[sb], 1);
         last = old == hi - lo;
-        // Every other arrival already happened: safe to reset for the next launch.
         if (last) __hip_atomic_store(&P.counters[sb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       const uint64_t bal = __ballot(last);
@@ -258,354 +211,343 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(DecodeParams P) {
       }
       if (lane == 0) s_nmerge = __popcll(bal);
     }
-    lds_barrier();  // also keeps partial loads below the arrivals
+    lds_barrier();
     const int nm = __builtin_amdgcn_readfirstlane(s_nmerge);
     if (in_loop) {
       for (int i = 0; i < nm; ++i) merge_partials<T, D>(P, s_merge[i][0], s_merge[i][1], s_merge[i][2]);
     } else {
       merge_queued<T, D>(P, s_merge, nm);
     }
-    lds_barrier();  // s_split / s_merge are free again
+    lds_barrier();
     nsplit = 0;
   };
 
-  for (int w = w0; w < N; w += N0) {
-  const int64_t p0 = R.start(w), p1 = R.start(w + 1);
-  const int len = (int)(p1 - p0);
-  lds_barrier();  // the previous range's readers are done with s_pid / s_q / s_bf / s_bl
-
-  // ---- round 2: the range's page ids (requested at the start for the first range when
-  // the page list is exactly indptr[B] long; otherwise now), written to LDS below ...
-  if (w != w0 || total != tg) {
+  int rmax = P.r_cap;  // ranges of this plan (from the first record; never past the workspace)
+  for (int w = w0; w < rmax; w += N0) {
+    const int32_t* rec = P.sched + (int64_t)w * kRecStride;
+    const int32_t* head = P.sched_head + (int64_t)w * kHeadWords;
+    lds_barrier();  // the previous range's readers of s_pid / s_seg / the query rows are done
+    // ---- round 1: the range's head: header and first segments (words 0..63), first 64 page ids
+    const int hv = head[lane];
+    const int pv = head[kHeadPidOff + lane];
+    const int rr = __builtin_amdgcn_readlane(hv, kHdrRanges);
+    rmax = rr < rmax ? rr : rmax;
+    int len = __builtin_amdgcn_readlane(hv, kHdrLen);
+    len = len < 0 ? 0 : (len > kRangePages ? kRangePages : len);
+    int nseg = __builtin_amdgcn_readlane(hv, kHdrNseg);
+    nseg = nseg < 0 ? 0 : (nseg > len ? len : nseg);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // round 1 complete (compiler-visible vmcnt(0))
+    if (w >= rmax) break;
+    if (nseg == 0) continue;
+    // segment s < kHeadSegs from the round-1 registers
+    auto seg_reg = [&](int s) __attribute__((always_inline)) -> int4 {
+      return make_int4(__builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s),
+                       __builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s + 1),
+                       __builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s + 2),
+                       __builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s + 3));
+    };
+    const int qs = min(nseg, qcap);
+    // ---- round 2 (copies into LDS): segment records, page ids, query rows of the first qs
+    // segments, then this wave's first unit.  Job k of the first three kinds is wave k % W's.
+    const int npj = (len + 255) / 256;
+    const int qchunks = qs * (qrow / 16);
+    const int nqj = (qchunks + 63) / 64;
+    const int njobs = 1 + npj + nqj;
+    for (int k = wave; k < njobs; k += W) {
+      if (k == 0) {
+        dma16(rec + kRecSegOff + 4 * lane, reinterpret_cast<const char*>(s_seg));
+      } else if (k <= npj) {
+        const int i = k - 1;
+        dma16(rec + kRecPidOff + 256 * i + 4 * lane, reinterpret_cast<const char*>(s_pid + 256 * i));
+      } else {
+        const int i = k - 1 - npj;
+        int c = 64 * i + lane;
+        c = c < qchunks ? c : qchunks - 1;
+        const int per = qrow / 16, s = c / per, r = c - s * per;
+        const int h = r / (D / 8), dc = r - h * (D / 8);
+        int4 sv = seg_reg(0);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {  // unconditional loads from clamped indices, as in round 1
-      const int t = threadIdx.x + r * NT;
-      pv[r] = P.indices[p0 + (t < len ? t : len - 1)];
-    }
-  }
-  // ... while all threads look up the range's sequences in the staged rows: the first and
-  // last sequence with pages in [p0, p1) and how many have any (the segments).
-  for (int i = threadIdx.x; i < B; i += NT) {
-    const int64_t s = s_indptr[i], e = s_indptr[i + 1];
-    if (e > s && e > p0 && s < p1) {
-      atomicAdd(&s_nseg, 1);
-      atomicMin(&s_bf, i);
-      atomicMax(&s_bl, i);
-    }
-  }
-  lds_barrier();
-  const int bf = rd(&s_bf, 0), nseg = rd(&s_nseg, 0);
-  if (nseg == 0) continue;  // pages before indptr[0]: no sequence owns them
-  const int nq = min(qseg, rd(&s_bl, 0) - bf + 1);  // sequences bf .. bf + nq - 1 get staged
-  const int per = P.hq * (D / 8);  // 16-byte q chunks per sequence
-  const int nqc = nq * per;        // <= 4 * NT: qseg * hq * D * 2 <= 32 KB
-  auto q_src = [&](int c) __attribute__((always_inline)) -> const T* {
-    const int i = c / per, rr = c - i * per;
-    const int hh = rr / (D / 8), d = (rr - hh * (D / 8)) * 8;
-    return qall + (bf + i) * P.q_sn + (int64_t)hh * P.q_sh + d;
-  };
-  auto write_pids = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {  // ids outside the pool are read as absent (-1)
-      const int t = threadIdx.x + r * NT;
-      if (t < len) s_pid[t] = ((int64_t)pv[r] >= 0 && (int64_t)pv[r] < P.num_pages) ? pv[r] : -1;
-    }
-  };
-  // Staged row i, head hh lives at s_q[(i * hq + hh) * D]: chunk c maps to c * 8.  When a
-  // thread stages at most one chunk (the common case) it is kept in a register and written
-  // after the first K/V loads are issued, so those do not wait for the q rows.
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (a plain vector: stays in registers)
-  const bool q_one = P.q_vec && nqc <= NT;
-  const u32x4 qc0 = *reinterpret_cast<const u32x4*>(
-      q_one ? q_src((int)threadIdx.x < nqc ? (int)threadIdx.x : nqc - 1)
-            : reinterpret_cast<const T*>(P.part_o));  // (unconditional: any aligned address)
-  if (!q_one && P.q_vec) {
-    u32x4 qc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = threadIdx.x + r * NT;
-      qc[r] = *reinterpret_cast<const u32x4*>(q_src(c < nqc ? c : nqc - 1));
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = threadIdx.x + r * NT;
-      if (c < nqc) *reinterpret_cast<u32x4*>(s_qw + (int64_t)c * 8) = qc[r];
-    }
-  } else if (!q_one) {
-    for (int c = threadIdx.x; c < nqc; c += NT) {
-      const T* src = q_src(c);
-#pragma unroll
-      for (int x = 0; x < 8; ++x) s_qw[(int64_t)c * 8 + x] = src[x];
-    }
-  }
-  write_pids();
-  // Pages before the first sequence (only when indptr[0] > 0) are skipped.
-  const int gap0 = (int)max((int64_t)rd(s_indptr, bf) - p0, (int64_t)0);
-  if (threadIdx.x < 8) s_next[threadIdx.x] = gap0;
-  lds_barrier();
-  if (threadIdx.x == 0) {  // (read by every thread before the barrier above)
-    s_nseg = 0;
-    s_bf = INT_MAX;
-    s_bl = -1;
-  }
-
-  // The J waves of a head split the range's pages, each in increasing order: by default
-  // wave j takes pages j, j + J, j + 2J, ... (a fixed split: the result is reproducible);
-  // with P.dynamic the waves take them on demand from the head's LDS counter, so a wave
-  // that gets fewer issue slots takes fewer pages and the J waves finish together.
-  int next_static = gap0 + j;
-  auto grab = [&]() __attribute__((always_inline)) -> int {  // next page of this head (uniform)
-    if (P.dynamic) {
-      int v = 0;
-      if (lane == 0) v = atomicAdd(&s_next[h], 1);
-      return __builtin_amdgcn_readfirstlane(v);
-    }
-    const int v = next_static;
-    next_static += J;
-    return v;
-  };
-  auto pid_at = [&](int i) __attribute__((always_inline)) -> int {  // id of range page i (uniform)
-    return __builtin_amdgcn_readfirstlane(s_pid[i < len ? i : len - 1]);
-  };
-  // ---- the range's pages, one loop per wave; sequence (segment) boundaries are crossed
-  // inside it.  Every wave ends each segment of the range once and in order, so the
-  // combine barriers match up even though waves reach them at different pages.
-  int b = bf - 1, si = -1;
-  int s1 = 0, last_len = 0, w_lo = 0, w_hi = 0;
-  int64_t seg_end = p0;
-  bool whole = false;
-  const bool qv = active && lr < g;
-  const T* qrow_lds = s_q;
-  f4 o[MT];
-  float m = -INFINITY, lsum = 0.f;
-
-  auto start_segment = [&]() __attribute__((always_inline)) {  // uniform across the workgroup
-    int s0;
-    do {
-      ++b;
-      s0 = rd(s_indptr, b);
-      s1 = rd(s_indptr, b + 1);
-    } while (s1 <= seg_end);  // skip sequences with no pages
-    ++si;
-    last_len = rd(s_lastlen, b);
-    last_len = last_len < 0 ? 0 : (last_len > 16 ? 16 : last_len);
-    seg_end = p1 < s1 ? p1 : s1;
-    w_lo = R.owner(s0);
-    w_hi = R.owner(s1 - 1);
-    whole = w_lo == w_hi;
-    // Q of this segment is read from LDS at every page (lane = head lr of the group,
-    // dims 32*s + 8*lg .. +7); a sequence past the staged ones fills the spare slot first.
-    int qslot = b - bf;
-    if (qslot >= nq) {
-      qslot = qseg;
-      lds_barrier();  // the spare slot's previous readers are done
-      for (int c = threadIdx.x; c < per; c += NT) {
-        const int hh = c / (D / 8), d = (c - hh * (D / 8)) * 8;
-        const T* src = qall + b * P.q_sn + (int64_t)hh * P.q_sh + d;
-        T* dst = s_qw + ((int64_t)(qseg * P.hq + hh)) * D + d;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) dst[x] = src[x];
+        for (int x = 1; x < 4; ++x) sv = s == x ? seg_reg(x) : sv;
+        const int b = unpack_seg(sv, len, B).b;
+        dma16(qall + (int64_t)b * P.q_sn + (int64_t)h * P.q_sh + 8 * dc, qarea + 1024 * i);
       }
-      lds_barrier();
     }
-    qrow_lds = s_q + ((int64_t)(qslot * P.hq + (active ? h * g + (qv ? lr : 0) : 0))) * D + 8 * lg;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) o[mt] = f4{0.f, 0.f, 0.f, 0.f};
-    m = -INFINITY;
-    lsum = 0.f;
-  };
+    if (threadIdx.x < W) s_next[threadIdx.x] = J;  // (pages 0 .. J-1 go to the ranks in order)
+    int pi = active ? j : len;  // this wave's current page (range page index)
+    int cpid = 0;
+    bool have = pi < len;
+    if (have) {
+      cpid = __builtin_amdgcn_readlane(pv, pi);
+      const int64_t pg = page_ok(cpid) ? cpid : 0;
+      issue_tile(kc, pg, kbuf, false);
+      issue_tile(vc, pg, vbuf, true);
+    }
+    if (have) wait_vm<2 * NI>(); else wait_vm<0>();
+    lds_barrier();
 
-  auto end_segment = [&]() __attribute__((always_inline)) {  // uniform across the workgroup
-    // Combine the J waves of each head, all of them at once: wave j owns the output tiles
-    // mt = j, j + J, ...  Every wave parks its (max, sum) and the tiles it does not own;
-    // then each wave folds the J copies of its own tiles.
-    if constexpr (J > 1) {
-      if (active) {
-        s_ml[(h * J + j) * 64 + lane] = make_float2(m, lsum);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int c = mt % J;
-          if (c != j) s_copy[((h * MT + mt) * (J - 1) + (j < c ? j : j - 1)) * 64 + lane] = o[mt];
-        }
+    // ---- per-segment state
+    int si = 0;
+    Seg sg;
+    auto seg_at = [&](int s) __attribute__((always_inline)) -> Seg {
+      int4 v;
+      if (s < kSegLds) {
+        v = s_seg[s];
+        v = make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                      __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+      } else {
+        v = *reinterpret_cast<const int4*>(rec + kRecSegOff + 4 * s);
+        v = make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                      __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
       }
-      lds_barrier();
-      if (active) {
-        float2 mls[J];
+      Seg sgv = unpack_seg(v, len, B);
+      // (a valid plan has w_lo <= w <= w_hi < R; clamped so a stale one cannot index past the
+      // partial slots)
+      sgv.whi = sgv.whi < rmax ? sgv.whi : rmax - 1;
+      sgv.wlo = sgv.wlo < sgv.whi ? sgv.wlo : sgv.whi;
+      return sgv;
+    };
+    uint4 qop[KS];
+    f4 o[MT];
+    float m = -INFINITY, lsum = 0.f;
+    auto start_segment = [&]() __attribute__((always_inline)) {
+      sg = seg_at(si);
+      // query operand: column lr's query head, dims of its own KV head only
+      uint4 qv[KSH];
+      if (si < qs) {
+        const char* src = qarea + si * qrow + qh * D * 2 + 16 * lg;
 #pragma unroll
-        for (int jj = 0; jj < J; ++jj) mls[jj] = s_ml[(h * J + jj) * 64 + lane];
-        float mx = -INFINITY;
+        for (int s = 0; s < KSH; ++s) qv[s] = *reinterpret_cast<const uint4*>(src + 64 * s);
+      } else {
+        const T* src = qall + (int64_t)sg.b * P.q_sn + (int64_t)qh * P.q_sh + 8 * lg;
 #pragma unroll
-        for (int jj = 0; jj < J; ++jj) mx = fmaxf(mx, mls[jj].x);
-        const float mu = mx == -INFINITY ? 0.f : mx;
-        float sc[J];
-        float ls = 0.f, cj = 0.f;
+        for (int s = 0; s < KSH; ++s) qv[s] = *reinterpret_cast<const uint4*>(src + 32 * s);
+      }
 #pragma unroll
-        for (int jj = 0; jj < J; ++jj) {
-          sc[jj] = __builtin_amdgcn_exp2f(mls[jj].x - mu);
-          ls += mls[jj].y * sc[jj];
-          cj = jj == j ? sc[jj] : cj;
+      for (int s = 0; s < KS; ++s) qop[s] = (colv && hn == s / KSH) ? qv[s % KSH] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) o[mt] = f4{0.f, 0.f, 0.f, 0.f};
+      m = -INFINITY;
+      lsum = 0.f;
+    };
+
+    auto end_segment = [&]() __attribute__((always_inline)) {
+      float ltot = lsum + __shfl_xor(lsum, 16, 64);
+      ltot += __shfl_xor(ltot, 32, 64);
+      const bool whole = sg.wlo == sg.whi;
+      float M = m, L = ltot;
+      if (J > 1) {
+        // (every read of the J copies is issued at once: slots past J repeat slot 0 and are
+        // dropped by the selects)
+        if (active && lg == 0) s_ml[wave][lr] = make_float2(m, ltot);
+        lds_barrier();
+        if (active) {
+          float2 v[W];
+#pragma unroll
+          for (int jj = 0; jj < W; ++jj) v[jj] = s_ml[hb + NHB * (jj < J ? jj : 0)][lr];
+          M = -INFINITY;
+#pragma unroll
+          for (int jj = 0; jj < W; ++jj) M = jj < J ? fmaxf(M, v[jj].x) : M;
+          const float mu = M == -INFINITY ? 0.f : M;
+          L = 0.f;
+#pragma unroll
+          for (int jj = 0; jj < W; ++jj) L += jj < J ? v[jj].y * __builtin_amdgcn_exp2f(v[jj].x - mu) : 0.f;
+          const float cs = __builtin_amdgcn_exp2f(m - mu);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) o[mt] *= cs;
         }
+        // tile mt is folded and written by rank mt % J of the head block
+        if (si == nseg - 1) {
+          // the range's last segment: no copy is in flight into any page buffer, so every wave
+          // parks all its tiles in its own buffer and one barrier covers the whole exchange
+          char* mine = smem + wave * 2 * TILE;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          if (mt % J != j) continue;
-          f4 cp[J - 1];
+          for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f4*>(mine + mt * 1024 + lane * 16) = o[mt];
+          lds_barrier();
 #pragma unroll
-          for (int jj = 0; jj < J - 1; ++jj) cp[jj] = s_copy[((h * MT + mt) * (J - 1) + jj) * 64 + lane];
-          f4 acc = o[mt] * cj;
-#pragma unroll
-          for (int jj = 0; jj < J - 1; ++jj) {
-            const int src = jj < j ? jj : jj + 1;  // wave rank that parked copy jj
-            float s2 = 0.f;
-#pragma unroll
-            for (int x = 0; x < J; ++x) s2 = x == src ? sc[x] : s2;
-            acc += cp[jj] * s2;
+          for (int mt = 0; mt < MT; ++mt) {
+            if (active && j == mt % J) {
+              o[mt] = fold_copies(J, [&](int jj) __attribute__((always_inline)) -> f4 {
+                return *reinterpret_cast<const f4*>(smem + (hb + NHB * jj) * 2 * TILE + mt * 1024 + lane * 16);
+              });
+            }
           }
-          o[mt] = acc;
+        } else {
+          // next units are in flight into the page buffers: one tile per step through two
+          // alternating exchange buffers (step mt + 2 rewrites a buffer only after the barrier
+          // of step mt + 1, which every reader of step mt has passed)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            s_x[mt & 1][wave][lane] = o[mt];
+            lds_barrier();
+            if (active && j == mt % J) {
+              o[mt] = fold_copies(J, [&](int jj) __attribute__((always_inline)) -> f4 {
+                return s_x[mt & 1][hb + NHB * jj][lane];
+              });
+            }
+          }
         }
-        m = mx;
-        lsum = ls;
       }
-    }
-    if (!whole && threadIdx.x == 0) {
-      s_split[nsplit][0] = b;
-      s_split[nsplit][1] = w_lo;
-      s_split[nsplit][2] = w_hi;
-    }
-    lds_barrier();  // slots are read before the next segment parks new states
-    float ltot = lsum + __shfl_xor(lsum, 16, 64);
-    ltot += __shfl_xor(ltot, 32, 64);
-    if (active && lr < g) {
-      const int hq = h * g + lr;
-      const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-      if (whole) {
-        T* orow = out + b * P.o_sn + (int64_t)hq * P.o_sh + 4 * lg;
+      if (!whole && threadIdx.x == 0) {
+        s_split[nsplit][0] = sg.b;
+        s_split[nsplit][1] = sg.wlo;
+        s_split[nsplit][2] = sg.whi;
+      }
+      if (colv) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        if (whole) {
+          T* orow = out + (int64_t)sg.b * P.o_sn + (int64_t)qh * P.o_sh + 4 * lg;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            if (mt % J != j) continue;
+            if (P.o_vec) {
+              *reinterpret_cast<uint2*>(orow + 16 * mt) = make_uint2(Mma<T>::pack(o[mt][0] * inv, o[mt][1] * inv),
+                                                                     Mma<T>::pack(o[mt][2] * inv, o[mt][3] * inv));
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) orow[16 * mt + i] = from_f32<T>(o[mt][i] * inv);
+            }
+          }
+        } else {
+          const int64_t slot = (int64_t)w + sg.b, sidx = slot * P.hq + qh;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            if (mt % J != j) continue;
+            st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), o[mt] * inv);
+          }
+          if (j == 0 && lg == 0) store_partial_ml(P, slot, qh, M, L);
+        }
+      }
+      lds_barrier();  // s_split / s_ml / s_x are read before the next segment writes them
+      if (!whole && ++nsplit == kMaxSplit) flush_splits(true);
+      ++si;
+      if (si < nseg) start_segment();
+    };
+
+    start_segment();
+    const float scale = P.scale_log2;
+    while (have) {
+      while (si < nseg && pi >= sg.end) end_segment();
+      if (si >= nseg) {  // (a page no segment covers: only for a malformed schedule)
+        wait_vm<0>();
+        break;
+      }
+      // K of unit pi has landed (its V may still be in flight)
+      wait_vm<NI>();
+      f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
+      const char* krow = kbuf + lr * RB;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint4 a = *reinterpret_cast<const uint4*>(krow + (((4 * s + lg) ^ kx<RB>(lr)) << 4));
+        sacc = Mma<T>::qk(a, qop[s], sacc);
+      }
+      // next page: fixed (rank j takes j, j+J, ...: reproducible) or, with PKV_DECODE_DYNAMIC,
+      // the head block's next page on demand (waves finish together; the summation order varies)
+      int nxt = pi + J;
+      if (P.dynamic) {
+        int v = 0;
+        if (lane == 0) v = atomicAdd(&s_next[hb], 1);
+        nxt = __builtin_amdgcn_readfirstlane(v);
+      }
+      const bool more = nxt < len;
+      int npid = 0;
+      if (more) npid = __builtin_amdgcn_readfirstlane(s_pid[nxt]);
+      wait_lgkm0();  // the K tile has been read: it can be refilled
+      if (more) issue_tile(kc, page_ok(npid) ? npid : 0, kbuf, false);
+      // softmax over the unit's 16 tokens (only a sequence's last page is partial)
+      int nv = pi == sg.end - 1 ? sg.nv : 16;
+      nv = page_ok(cpid) ? nv : 0;
+      float sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = (4 * lg + i < nv) ? sacc[i] : -INFINITY;
+      float cmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      const float cms = cmax * scale;
+      const bool grow = cms > m + kLazyMax;  // (false while every score so far is masked)
+      if (__ballot(grow)) {
+        const float mnew = grow ? cms : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[mt] *= alpha;
+        lsum *= alpha;
+        m = mnew;
+      }
+      const float nmu = m == -INFINITY ? 0.f : -m;
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], scale, nmu));
+      lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      const uint2 pb = make_uint2(Mma<T>::pack(pr[0], pr[1]), Mma<T>::pack(pr[2], pr[3]));
+      // V of unit pi has landed (the next unit's K may still be in flight)
+      if (more) wait_vm<NI>(); else wait_vm<0>();
+      if (nv < 16) {  // rows past the sequence's end read as zeros (0 * NaN would poison P.V)
+        for (int c = lane; c < (16 - nv) * CPR; c += 64)
+          *reinterpret_cast<uint4*>(vbuf + nv * RB + 16 * c) = make_uint4(0, 0, 0, 0);
+      }
+      const int tr_row = 4 * lg + (lr >> 2);
+      const char* trb = vbuf + tr_row * RB + (lr & 1) * 8;
+      if constexpr (HB == 1) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          if (mt % J != j) continue;
-          if (P.o_vec) {
-            const uint2 pk = make_uint2(Mma<T>::pack(o[mt][0] * inv, o[mt][1] * inv),
-                                        Mma<T>::pack(o[mt][2] * inv, o[mt][3] * inv));
-            *reinterpret_cast<uint2*>(orow + 16 * mt) = pk;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) orow[16 * mt + i] = from_f32<T>(o[mt][i] * inv);
-          }
+          const int chunk = (2 * mt + ((lr & 3) >> 1)) ^ vx<RB>(tr_row);
+          o[mt] = Mma<T>::pv(lds_read_tr16(trb + (chunk << 4)), pb, o[mt]);
         }
       } else {
-        const int64_t sidx = ((int64_t)w + b) * P.hq + hq;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          if (mt % J != j) continue;
-          st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), o[mt] * inv);
+        for (int u = 0; u < HB / 2; ++u) {
+          const uint2 p0 = hn == 2 * u ? pb : make_uint2(0, 0);
+          const uint2 p1 = hn == 2 * u + 1 ? pb : make_uint2(0, 0);
+          const uint4 pp = make_uint4(p0.x, p0.y, p1.x, p1.y);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int c0 = ((2 * u) * D) / 8 + 2 * mt + ((lr & 3) >> 1);
+            const int c1 = c0 + D / 8;
+            const uint2 va = lds_read_tr16(trb + ((c0 ^ vx<RB>(tr_row)) << 4));
+            const uint2 vb = lds_read_tr16(trb + ((c1 ^ vx<RB>(tr_row)) << 4));
+            o[mt] = Mma<T>::qk(make_uint4(va.x, va.y, vb.x, vb.y), pp, o[mt]);
+          }
         }
-        if (j == 0 && lg == 0) store_partial_ml(P, sidx, m, ltot);
       }
+      wait_lgkm0();  // the V tile has been read: it can be refilled
+      if (more) issue_tile(vc, page_ok(npid) ? npid : 0, vbuf, true);
+      pi = nxt;
+      cpid = npid;
+      have = more;
     }
-    if (!whole && ++nsplit == kMaxSplit) flush_splits(true);
-  };
-  auto advance = [&]() __attribute__((always_inline)) {
-    end_segment();
-    start_segment();
-  };
-
-  auto process = [&](const uint4 (&kr)[KSTEPS], const uint4 (&vr)[VCH], int64_t gp, int pgid) __attribute__((always_inline)) {
-    int nv = (gp == s1 - 1) ? last_len : 16;
-    if (pgid < 0) nv = 0;
-    // Stage V first (tokens past the end zeroed: 0 * NaN would poison P.V); only a
-    // sequence's last page can be partial.
-    if (nv == 16) {
-#pragma unroll
-      for (int r = 0; r < VCH; ++r) {
-        const int c = lane + 64 * r, t = c / CPR, cc = c % CPR;
-        *reinterpret_cast<uint4*>(vtile + t * ROWB + ((cc ^ vswz<D>(t)) << 4)) = vr[r];
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < VCH; ++r) {
-        const int c = lane + 64 * r, t = c / CPR, cc = c % CPR;
-        const uint4 val = t < nv ? vr[r] : make_uint4(0, 0, 0, 0);
-        *reinterpret_cast<uint4*>(vtile + t * ROWB + ((cc ^ vswz<D>(t)) << 4)) = val;
-      }
-    }
-    f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      uint4 qs = *reinterpret_cast<const uint4*>(qrow_lds + 32 * s);
-      qs = qv ? qs : make_uint4(0, 0, 0, 0);
-      sacc = Mma<T>::qk(kr[s], qs, sacc);
-    }
-    float sv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sv[i] = (4 * lg + i < nv) ? sacc[i] * P.scale_log2 : -INFINITY;
-    float cmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-    const float mnew = fmaxf(m, cmax);
-    const float muse = mnew == -INFINITY ? 0.f : mnew;
-    // v_exp_f32 directly: arguments are <= 0, results in [0, 1] (denormals flush to 0).
-    const float alpha = __builtin_amdgcn_exp2f(m - muse);
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(sv[i] - muse);
-    lsum = lsum * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    // Rescale the accumulator only when some head's running max moved (rare after the
-    // first pages of a sequence).
-    if (__ballot(mnew != m)) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) o[mt] *= alpha;
-    }
-    m = mnew;
-    __builtin_amdgcn_wave_barrier();
-    const uint2 pb = make_uint2(Mma<T>::pack(pr[0], pr[1]), Mma<T>::pack(pr[2], pr[3]));
-    const int tr_row = 4 * lg + (lr >> 2);
-    const char* tr_base = vtile + tr_row * ROWB + (lr & 1) * 8;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int chunk = (2 * mt + ((lr & 3) >> 1)) ^ vswz<D>(tr_row);
-      o[mt] = Mma<T>::pv(lds_read_tr16(tr_base + (chunk << 4)), pb, o[mt]);
-    }
-    __builtin_amdgcn_wave_barrier();
-  };
-
-  // One step: consume range page idx from the buffer, then take the head's next page and
-  // request it into the same buffer.  The next page's id is read from LDS before the compute,
-  // so its request does not wait for that read afterwards (0.2 us per launch).
-  auto step = [&](uint4 (&kr)[KSTEPS], uint4 (&vr)[VCH], int& idx) __attribute__((always_inline)) {
-    const int64_t gp = p0 + idx;
-    while (gp >= seg_end) advance();
-    const int nidx = grab();
-    const int cpid = pid_at(idx), npid = pid_at(nidx);
-    process(kr, vr, gp, cpid);
-    idx = nidx;
-    load_page(npid, kr, vr);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  start_segment();
-  // A wave's pages come in increasing order, so the first one past the range ends its loop.
-  int ia = len;
-  if (active) ia = grab();
-  load_page(pid_at(ia), kA, vA);
-  if (q_one && (int)threadIdx.x < nqc) *reinterpret_cast<u32x4*>(s_qw + (int64_t)threadIdx.x * 8) = qc0;
-  lds_barrier();  // the q rows are staged
-  while (ia < len) step(kA, vA, ia);
-  while (si < nseg - 1) advance();
-  end_segment();
+    while (si < nseg) end_segment();
   }  // ranges
   if (nsplit > 0) flush_splits(false);
+  // output rows of sequences that own no page
+  const int ne = P.sched_hdr[kGhEmpty];
+  for (int e = blockIdx.x; e < ne && e < B; e += gridDim.x) {
+    int b = P.sched_hdr[kGlobHdr + e];
+    if (b < 0 || b >= B) continue;
+    for (int x = threadIdx.x; x < P.hq * D; x += NT) {
+      const int h = x / D, d = x - h * D;
+      out[(int64_t)b * P.o_sn + (int64_t)h * P.o_sh + d] = from_f32<T>(0.f);
+    }
+  }
 }
 
-template <typename T, int D>
-int launch_mfma(const DecodeParams& P, hipStream_t s) {
-  constexpr int W = 8;
-  const MfmaLds L = mfma_lds<D, W>(P.hkv, P.hq, mfma_qseg(P.hq, D));
-  const dim3 grid(P.num_ctas), block(W * 64);
-  switch (W / P.hkv) {  // 1 <= hkv <= 8: J is 8, 4, 2 or 1
-    case 8: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 8>), grid, block, L.total, s, P); break;
-    case 4: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 4>), grid, block, L.total, s, P); break;
-    case 2: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 2>), grid, block, L.total, s, P); break;
-    default: hipLaunchKernelGGL((decode_mfma_kernel<T, D, W, 1>), grid, block, L.total, s, P); break;
-  }
+// Head block: the largest power of two HB with HB * g <= 16, HB * D <= 256 and HB | Hkv.
+int head_block(int d, int g, int hkv) {
+  int hb = 1;
+  while (2 * hb * g <= 16 && 2 * hb * d <= 256 && hkv % (2 * hb) == 0) hb *= 2;
+  return hb;
+}
+
+template <typename T, int D, int HB>
+int launch(const DecodeParams& P, hipStream_t s) {
+  constexpr int lds = Shape<HB, D>::LDS;
+  hipLaunchKernelGGL((decode_mfma_kernel<T, D, HB>), dim3(P.num_ctas), dim3(NT), lds, s, P);
   return (int)hipGetLastError();
+}
+
+template <typename T>
+int launch_t(const DecodeParams& P, int d, hipStream_t s) {
+  const int hb = head_block(d, P.hq / P.hkv, P.hkv);
+  if (d == 128) return hb == 2 ? launch<T, 128, 2>(P, s) : launch<T, 128, 1>(P, s);
+  return hb == 4 ? launch<T, 64, 4>(P, s) : (hb == 2 ? launch<T, 64, 2>(P, s) : launch<T, 64, 1>(P, s));
 }
 
 }  // namespace
@@ -613,14 +555,15 @@ int launch_mfma(const DecodeParams& P, hipStream_t s) {
 namespace pkv {
 
 bool decode_mfma_supported(int dtype, int d, int g, int hkv, int batch) {
-  return (dtype == kF16 || dtype == kBF16) && (d == 64 || d == 128) && g >= 1 && g <= 16 &&
-         hkv >= 1 && hkv <= 8 && batch <= kMetaCap;
+  (void)batch;
+  if (!((dtype == kF16 || dtype == kBF16) && (d == 64 || d == 128) && g >= 1 && g <= 16 && hkv >= 1))
+    return false;
+  return hkv / head_block(d, g, hkv) <= W;
 }
 
 int decode_mfma_dispatch(const DecodeParams& P, int dtype, int d, hipStream_t s) {
   if (P.ps != 16) return decode_valu_dispatch(P, dtype, d, s);
-  if (dtype == kF16) return d == 64 ? launch_mfma<_Float16, 64>(P, s) : launch_mfma<_Float16, 128>(P, s);
-  return d == 64 ? launch_mfma<__hip_bfloat16, 64>(P, s) : launch_mfma<__hip_bfloat16, 128>(P, s);
+  return dtype == kF16 ? launch_t<_Float16>(P, d, s) : launch_t<__hip_bfloat16>(P, d, s);
 }
 
 }  // namespace pkv

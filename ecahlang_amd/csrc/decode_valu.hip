@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams P) {
             int64_t s = slot * P.hq + hq;
 #pragma unroll
             for (int j = 0; j < DPL; ++j) st_dev(P.part_o + s * D + lane * DPL + j, o[gi][j] * inv);
-            if (lane == 0) store_partial_ml(P, s, m[gi], l[gi]);
+            if (lane == 0) store_partial_ml(P, slot, hq, m[gi], l[gi]);
           }
         }
       }

@@ -50,7 +50,7 @@ def _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, ro
         raise NotImplementedError("in-kernel RoPE is not implemented")
 
 
-_DECODE_VALU, _DECODE_DYNAMIC = 1, 2  # pkv_batch_decode flags (include/pagedkv.h)
+_DECODE_VALU, _DECODE_DYNAMIC, _DECODE_PLANNED = 1, 2, 4  # pkv_batch_decode flags (include/pagedkv.h)
 
 class BatchDecodeWithPagedKVCacheWrapper:
     """Paged decode attention: one query token per sequence (FlashInfer contract)."""
@@ -128,6 +128,15 @@ class BatchDecodeWithPagedKVCacheWrapper:
                                                   stream_ptr(dev)), "decode plan")
             self._counters_ready = self._batch
         self._flags = 0 if deterministic else _DECODE_DYNAMIC
+        if self._mfma:
+            # the matrix-core kernel's schedule, built on the device from this page table
+            check(lib().pkv_decode_plan(self._indptr.data_ptr(), self._indices.data_ptr(),
+                                        self._indices.numel(), self._last.data_ptr(), self._batch,
+                                        self._hq, self._hkv, self._d, self._ps, self._ctas,
+                                        self._workspace.data_ptr(),
+                                        self._workspace.numel() * self._workspace.element_size(),
+                                        stream_ptr(dev)), "decode plan")
+            self._flags |= _DECODE_PLANNED
         self._planned = True
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,

@@ -102,8 +102,8 @@ int pkv_append_paged_kv_cache_rope(const void* q, int64_t q_stride_n, int64_t q_
                                    int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                    int32_t dtype, int32_t* err_count, void* stream);
 
-/* Workspace bytes pkv_batch_decode needs for this geometry (num_indices = length of the
- * kv_indices buffer): the host half of BatchDecodeWithPagedKVCacheWrapper.plan
+/* Workspace bytes pkv_decode_plan and pkv_batch_decode need for this geometry (num_indices =
+ * length of the kv_indices buffer): the host half of BatchDecodeWithPagedKVCacheWrapper.plan
  * (ecahlang/main.py:341-347, :444-455).  The reference hands the wrapper a 128 MiB buffer
  * (ecahlang/main.py:203). */
 int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
@@ -114,9 +114,25 @@ int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t 
  * buffer is fresh or the batch grows. */
 int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream);
 
-/* 1 when pkv_batch_decode runs the matrix-core kernel for this shape (fp16/bf16, head_dim 64
- * or 128, page_size 16, group <= 16, num_kv_heads <= 8, batch <= 2048), 0 when it runs the
- * vector-ALU kernel. */
+/* The device half of BatchDecodeWithPagedKVCacheWrapper.plan (ecahlang/main.py:341-347,
+ * :444-455, :538-548): one kernel reads the page table (kv_indptr, kv_indices, kv_last_page_len)
+ * and writes the matrix-core kernel's schedule into the workspace: the batch's pages cut into
+ * ranges (about one per workgroup, at most 512 pages each; a range that holds a sequence start
+ * gets fewer pages, since its waves combine their states there), each with its sequence
+ * segments and a copy of its page ids.  FlashInfer's plan computes its schedule on the host after copying
+ * kv_indptr back; this one never synchronises and can be captured.  Every decode launch on the
+ * same workspace with PKV_DECODE_PLANNED reads it, so the page table it was built from must not
+ * change before those launches (re-plan after rebuilding it, as the reference does before each
+ * step). */
+int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
+                    const int32_t* kv_last_page_len, int32_t batch, int32_t num_qo_heads,
+                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t num_ctas,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* 1 when pkv_batch_decode can run the matrix-core kernel for this shape (fp16/bf16, head_dim
+ * 64 or 128, group <= 16, and num_kv_heads at most 8 head blocks of up to 256 / head_dim heads;
+ * page_size 16 and 16-byte aligned q rows are checked per call), 0 when it runs the vector-ALU
+ * kernel. */
 int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
                          int32_t num_kv_heads, int32_t batch);
 
@@ -125,15 +141,17 @@ int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
  * seq_len_b = (npages_b - 1) * page_size + kv_last_page_len[b] tokens of sequence b, with
  * KV head h / (num_qo_heads / num_kv_heads); fp32 accumulation, output in `dtype`.  A
  * sequence with no tokens yields zeros.  num_ctas workgroups each stream an equal share of
- * the batch's pages.  flags: PKV_DECODE_VALU selects the vector-ALU kernel (cross-checks);
- * PKV_DECODE_DYNAMIC lets the waves of a workgroup take pages on demand instead of in a
- * fixed order (a little faster; the summation order, and so the last bits of the result,
- * then vary from call to call).  Without it the result is bitwise reproducible for a given
- * num_ctas.  Page ids outside [0, num_pages) and page-list entries past num_indices are
- * never read (their tokens are treated as absent); pages before kv_indptr[0] belong to no
- * sequence. */
+ * the batch's pages.  flags: PKV_DECODE_PLANNED says pkv_decode_plan has written this page
+ * table's schedule into the workspace (same batch, num_indices and num_ctas), which the
+ * matrix-core kernel needs; without it the vector-ALU kernel runs.  PKV_DECODE_VALU selects the
+ * vector-ALU kernel (cross-checks); PKV_DECODE_DYNAMIC lets that kernel's waves take pages on
+ * demand (the summation order, and so the last bits of the result, then vary from call to
+ * call).  Otherwise the result is bitwise reproducible for a given num_ctas.  Page ids outside
+ * [0, num_pages) and page-list entries past num_indices are never read (their tokens are
+ * treated as absent); pages before kv_indptr[0] belong to no sequence. */
 #define PKV_DECODE_VALU 1
 #define PKV_DECODE_DYNAMIC 2
+#define PKV_DECODE_PLANNED 4
 int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k_cache,
                      const void* v_cache, int64_t page_stride, int64_t num_pages,
                      const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,

@@ -70,7 +70,29 @@ def test_workspace_sizing_is_host_only():
     assert n >= (256 + 64) * 16 * 128 * 4
     assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 64) == 1
     assert _lib.lib().pkv_decode_uses_mfma(2, 64, 32, 8, 4) == 0
-    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 4096) == 0
+    # no batch limit (the schedule replaces the page-table rows staged in LDS)
+    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 16, 2, 4096) == 1
+    # head blocks: 32 KV heads of head_dim 128 at group 1 are 16 blocks of two, over the 8 waves
+    assert _lib.lib().pkv_decode_uses_mfma(0, 128, 32, 32, 4) == 0
+    assert _lib.lib().pkv_decode_uses_mfma(1, 128, 32, 8, 4) == 1
+
+
+def test_split_partial_ml_slots_are_whole_cache_lines():
+    # Each split segment's (max, sum) slot covers whole 128-byte lines (16 float2), so a merger
+    # never pulls another sequence's slot into its L2 before that slot is written.  Between
+    # 8 and 16 q heads the (max, sum) area must not grow; only the partial rows (D floats per
+    # head and slot) do.
+    from ecahlang_amd import _lib
+
+    a256 = lambda x: -(-x // 256) * 256
+    batch, d, ctas, nidx = 64, 128, 256, 12000
+    slots = max(ctas, -(-nidx // 512)) + batch
+    ws = lambda hq: _lib.lib().pkv_decode_workspace_bytes(batch, hq, d, ctas, nidx)
+    for hq in range(9, 17):
+        assert ws(hq) - ws(hq - 1) == a256(slots * hq * d * 4) - a256(slots * (hq - 1) * d * 4)
+    # crossing a multiple of 16 heads adds exactly one line per slot
+    assert ws(17) - ws(16) == (a256(slots * 17 * d * 4) - a256(slots * 16 * d * 4)
+                               + a256(slots * 32 * 8) - a256(slots * 16 * 8))
 
 
 def test_flashinfer_namespace_covers_reference_call_sites():
