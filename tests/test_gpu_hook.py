@@ -11,14 +11,14 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _model():
+def _model(dtype=torch.float16):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
     torch.manual_seed(0)
     cfg = Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                       num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=2048,
                       initializer_range=0.2)
-    return Qwen2ForCausalLM(cfg).to(DEV, torch.float16).eval()
+    return Qwen2ForCausalLM(cfg).to(DEV, dtype).eval()
 
 
 def _set_impl(model, name):
@@ -35,13 +35,16 @@ def _close(got, ref, what):
 
 
 @torch.no_grad()
-def test_hook_prefill_and_decode_match_sdpa_model():
+@pytest.mark.parametrize("model_dtype", [torch.float16, torch.float32])
+def test_hook_prefill_and_decode_match_sdpa_model(model_dtype):
+    """fp16 model over an fp16 cache; and an fp32 model over the fp16 cache, where the hook
+    casts q/k/v to the cache's dtype and the output back (main.py:50-53, 95-96)."""
     from ecahlang_amd import hook
     from ecahlang_amd.manager import AutoKVCacheManager
     from ecahlang_amd.wrappers import BatchDecodeWithPagedKVCacheWrapper, BatchPrefillWithPagedKVCacheWrapper
 
     hook.register()
-    model = _model()
+    model = _model(model_dtype)
     L, hkv, hq, d = 2, 2, 4, 64
     mgr = AutoKVCacheManager(L, hkv, d, vocab_size=512, dtype=torch.float16, device=DEV,
                              total_gpu_mem_bytes=300 * 16 * hkv * d * 2 * 2 * L, mem_utilization=1.0)

@@ -263,3 +263,59 @@ def test_prefix_sharing_matches_oracle(seed):
             _same_state(dev, ref)
     _same_state(dev, ref)
     assert dev.pool_errors() == 0
+
+
+def test_uncached_append_matches_oracle_and_cached_path():
+    """manager.py:167-185, the uncached append (metadata, seq lens, positions and the scatter in
+    one call): bitwise over the whole NaN-poisoned pool against the oracle's scatter on the
+    oracle manager's page tables, and against the cached path on a second pool."""
+    P, hkv, d, dt = 90, 2, 64, torch.float16
+    gen = torch.Generator().manual_seed(21)
+    lens = [5, 16, 33, 1, 70]       # allocated tokens; the last `new` of each are this call's
+    new = [5, 3, 33, 1, 2]
+    ids = [f"u{i}" for i in range(len(lens))]
+    pools = [_pool(P, hkv=hkv, d=d, stride=8) for _ in range(2)]
+    ref = RefKVCacheManager(P)
+    for m in pools:
+        m.kv_cache.view(torch.int16).fill_(0x7E00)  # NaN in fp16: untouched slots stay NaN
+    for sid, n in zip(ids, lens):
+        for m in pools:
+            m.allocate(sid, n)
+        ref.allocate(sid, n)
+    nnz = sum(new)
+    k = (torch.randn(nnz, hkv, d, generator=gen) * 0.5).to(dt)
+    v = (torch.randn(nnz, hkv, d, generator=gen) * 0.5).to(dt)
+    append_indptr = torch.tensor(np.concatenate([[0], np.cumsum(new)]), dtype=torch.int32, device=DEV)
+    pools[0].append_paged_kv_cache(ids, k.to(DEV), v.to(DEV), append_indptr, 0)
+    pools[1].prepare_append_metadata(ids, append_indptr)
+    pools[1].append_paged_kv_cache_cached(k.to(DEV), v.to(DEV), 0)
+    torch.cuda.synchronize()
+    idx, ptr, last = ref.get_append_metadata(ids)
+    sl = kv_ref.seq_lens(ptr, last, 16)
+    bidx, pos = kv_ref.batch_indices_positions(append_indptr.cpu().numpy(), sl, nnz)
+    want = kv_ref.append(np.full(pools[0].kv_cache[0].shape, 0x7E00, dtype=np.int16), k.view(torch.int16).numpy(),
+                         v.view(torch.int16).numpy(), bidx, pos, np.asarray(idx), np.asarray(ptr), 16)
+    got = [m.kv_cache[0].view(torch.int16).cpu().numpy() for m in pools]
+    assert np.array_equal(got[0], want)
+    assert np.array_equal(got[1], want)
+    assert all(m.pool_errors() == 0 for m in pools)
+
+
+def test_default_pool_sizing_from_free_device_memory():
+    """manager.py:38-49: without total_gpu_mem_bytes the pool is sized from the device's free
+    memory: max_blocks = int(free * mem_utilization) // (layers * 16 * Hkv * D * es * 2)."""
+    L, hkv, d, vocab, util = 2, 2, 64, 64, 0.002
+    # the constructor's first allocation (the penalty table) must come from torch's cache, so
+    # that the free memory it reads is the one read here
+    torch.ones(128, vocab, dtype=torch.float16, device=DEV)
+    torch.cuda.synchronize()
+    free = torch.cuda.mem_get_info(DEV.index or 0)[0]
+    m = AutoKVCacheManager(L, hkv, d, vocab_size=vocab, dtype=torch.float16, device=DEV, mem_utilization=util)
+    per_block = 16 * hkv * d * 2 * 2
+    assert m.max_blocks == int(free * util) // (L * per_block)
+    assert m.kv_cache.shape == (L, m.max_blocks, 2, 16, hkv, d)
+    assert len(m.free_blocks) == m.max_blocks
+    # the pool hands out its last pages first, as the reference's free list does
+    assert list(m.allocate("a", 40)) == [m.max_blocks - 1, m.max_blocks - 2, m.max_blocks - 3]
+    m.free("a")
+    assert m.pool_errors() == 0
