@@ -22,7 +22,9 @@ Printed JSON line:
 roofline.traffic is the decode kernel's HBM bytes per launch measured with hardware counters
 (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over `bench.py --profile-launches N`, each
 scaled by the same counter's reading for a plain copy of known size run in the same
-process); it is read from profiles/decode_traffic.json, where those runs were recorded.
+process); it is read from profiles/decode_traffic.json, where those runs were recorded, and is
+reported only when that record was taken on this workload and on these exact decode kernel
+sources (a SHA-256 over them), null otherwise.
 """
 from __future__ import annotations
 
@@ -53,15 +55,32 @@ def append_bytes(wb) -> int:
     return nnz * (4 * wb.hkv * wb.d * es + 12)
 
 
+DECODE_SOURCES = ("decode.hip", "decode_mfma.hip", "decode_plan.hip", "decode_sched.h", "attn_common.h",
+                  "mfma_common.h", "common.h")
+
+
+def decode_source_hash() -> str:
+    """SHA-256 over the matrix-core decode path's sources (the kernel, its schedule and the
+    shared headers), so a counter record is only used for the code it was taken on."""
+    import hashlib
+    h = hashlib.sha256()
+    root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ecahlang_amd", "csrc")
+    for name in DECODE_SOURCES:
+        with open(os.path.join(root, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
 def measured_traffic(wb, w):
     """HBM bytes per decode launch from the committed counter runs, when they were taken on
-    this workload and kernel (None otherwise)."""
+    this workload, this workgroup count and these decode sources (None otherwise)."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("decode_bytes") != decode_bytes(wb) or t.get("decode_ctas") != w._ctas:
+    if (t.get("decode_bytes") != decode_bytes(wb) or t.get("decode_ctas") != w._ctas
+            or t.get("decode_source_sha256") != decode_source_hash()):
         return None
     return t.get("traffic_bytes")
 
