@@ -10,6 +10,7 @@
 //   [part_o: f32 x (R+batch) x Hq x D]  (each part_ml slot is whole 128-byte lines)
 //   [schedule: global header + empty list (kGlobHdr + batch int32), R heads of kHeadWords
 //    int32, R records of kRecStride int32, plan scratch rank[batch], first-sequence[R] and range starts[R + 1]]
+#include <mutex>
 #include "attn_common.h"
 #include "decode_sched.h"
 #include "../../include/pagedkv.h"
@@ -146,4 +147,80 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
       decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
     return decode_mfma_dispatch(P, dtype, head_dim, s);
   return decode_valu_dispatch(P, dtype, head_dim, s);
+}
+
+// ---- allocation-free variant: the workspace is a file-scope device array
+
+namespace {
+
+// Scratch for pkv_batch_decode_noalloc: counters, split partials and the schedule of one call.
+// Every device the library runs on holds its own copy until the process ends.
+constexpr size_t kNoAllocScratchBytes = (size_t)PKV_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// Device address of this device's `scratch`, looked up once per device with that device current
+// (host code never passes the symbol itself to a kernel: on the host it is only a stand-in).
+int scratch_for(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return kBadArg;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return (int)e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return (int)e;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return kOk;
+}
+
+}  // namespace
+
+extern "C" int pkv_batch_decode_noalloc(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                        const void* k_cache, const void* v_cache, int64_t page_stride,
+                                        int64_t num_pages, const int32_t* kv_indptr,
+                                        const int32_t* kv_indices, int64_t num_indices,
+                                        const int32_t* kv_last_page_len, int32_t batch,
+                                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t page_size, float sm_scale, int32_t num_ctas, void* out,
+                                        int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
+                                        void* stream) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_ctas <= 0) return kBadArg;
+  if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
+  // sizes beyond the array are refused before anything is enqueued
+  if (ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices).total > kNoAllocScratchBytes)
+    return kWorkspaceTooSmall;
+  hipDevice_t dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  void* ws = nullptr;
+  int rc = scratch_for((int)dev, &ws);
+  if (rc) return rc;
+  const int64_t ws_bytes = (int64_t)kNoAllocScratchBytes;
+  // The array keeps the previous call's contents: the split counters start every call at zero
+  // (a fill kernel, not a memset node, so the call can also be captured).
+  if ((rc = pkv_decode_workspace_init(ws, batch, stream))) return rc;
+  int flags = 0;
+  if (page_size == 16 && num_qo_heads % num_kv_heads == 0 &&
+      decode_mfma_supported(dtype, head_dim, num_qo_heads / num_kv_heads, num_kv_heads, batch)) {
+    if ((rc = pkv_decode_plan(kv_indptr, kv_indices, num_indices, kv_last_page_len, batch, num_qo_heads,
+                              num_kv_heads, head_dim, page_size, num_ctas, ws, ws_bytes, stream)))
+      return rc;
+    flags = PKV_DECODE_PLANNED;
+  }
+  return pkv_batch_decode(q, q_stride_n, q_stride_h, k_cache, v_cache, page_stride, num_pages, kv_indptr,
+                          kv_indices, num_indices, kv_last_page_len, batch, num_qo_heads, num_kv_heads,
+                          head_dim, page_size, sm_scale, num_ctas, ws, ws_bytes, out, o_stride_n,
+                          o_stride_h, dtype, flags, stream);
 }

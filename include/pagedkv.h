@@ -161,6 +161,25 @@ int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, cons
                      int64_t workspace_bytes, void* out, int64_t o_stride_n, int64_t o_stride_h,
                      int32_t dtype, int32_t flags, void* stream);
 
+/* pkv_decode_plan + pkv_batch_decode in one call that allocates nothing and takes no workspace:
+ * the counters, split partials and schedule live in a file-scope device array of
+ * PKV_NOALLOC_SCRATCH_BYTES per device, held by every device the library runs on until the
+ * process ends.  No counterpart in the reference (FlashInfer's wrappers take a workspace): it is
+ * for callers that cannot allocate or own a workspace, such as code under graph capture or a
+ * tight serving loop.  Arguments as pkv_batch_decode (num_ctas workgroups); the result is bitwise
+ * the same as pkv_decode_plan + pkv_batch_decode with the same num_ctas.  Returns PKV_E_WORKSPACE,
+ * enqueueing nothing, when this geometry needs more than the array holds
+ * (pkv_decode_workspace_bytes > PKV_NOALLOC_SCRATCH_BYTES).  All calls on one device share that
+ * device's array, so calls that overlap on one device (another stream, another thread) race. */
+#define PKV_NOALLOC_SCRATCH_BYTES (16 << 20)
+int pkv_batch_decode_noalloc(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                             const void* k_cache, const void* v_cache, int64_t page_stride,
+                             int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
+                             int64_t num_indices, const int32_t* kv_last_page_len, int32_t batch,
+                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, float sm_scale, int32_t num_ctas, void* out,
+                             int64_t o_stride_n, int64_t o_stride_h, int32_t dtype, void* stream);
+
 /* BatchPrefillWithPagedKVCacheWrapper.run(q, paged_kv_cache) after
  * plan(qo_indptr, kv_indptr, kv_indices, kv_last_page_len, ..., causal=...)
  * (ecahlang/main.py:432-443, :68), vector-ALU kernel: query row i of request b

@@ -112,3 +112,16 @@ def test_attention_hook_registers_with_transformers():
 
     hook.register()
     assert AttentionInterface._global_mapping.get(hook.HOOK_NAME) is hook.ecah_attention
+
+
+def test_noalloc_decode_refuses_geometry_beyond_its_array():
+    # A page list long enough to need more ranges than the 16 MiB array holds: refused with the
+    # workspace error before anything is enqueued (no device call is made, so this runs on the
+    # CPU with null pointers).
+    from ecahlang_amd import _lib
+
+    L = _lib.lib()
+    assert L.pkv_decode_workspace_bytes(64, 16, 128, 256, 10_000_000) > (16 << 20)
+    rc = L.pkv_batch_decode_noalloc(None, 0, 0, None, None, 0, 0, None, None, 10_000_000, None, 64, 16, 2, 128,
+                                    16, 0.1, 256, None, 0, 0, 0, None)
+    assert rc == -6
