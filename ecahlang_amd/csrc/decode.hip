@@ -21,7 +21,7 @@ namespace pkv {
 int decode_plan_launch(const int32_t* indptr, const int32_t* indices, int64_t num_indices,
                        const int32_t* last, int batch, int num_ctas, int page_size, int seg_cost,
                        int r_cap, int32_t* ghdr, int32_t* recs, int32_t* heads, int32_t* rank,
-                       int32_t* bf, int32_t* starts, hipStream_t s);
+                       int32_t* bf, int32_t* starts, int32_t* swin, hipStream_t s);
 }
 
 namespace {
@@ -29,7 +29,7 @@ namespace {
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t cnt, ml, o, ghdr, heads, recs, rank, bf, starts, total;
+  size_t cnt, ml, o, ghdr, heads, recs, rank, bf, starts, swin, total;
   int64_t rcap;
 };
 inline WsLayout ws_layout(int batch, int hq, int d, int ctas, int64_t num_indices) {
@@ -45,7 +45,8 @@ inline WsLayout ws_layout(int batch, int hq, int d, int ctas, int64_t num_indice
   L.rank = L.recs + align256(sizeof(int32_t) * (size_t)L.rcap * kRecStride);
   L.bf = L.rank + align256(sizeof(int32_t) * (size_t)batch);
   L.starts = L.bf + align256(sizeof(int32_t) * (size_t)L.rcap);
-  L.total = L.starts + align256(sizeof(int32_t) * ((size_t)L.rcap + 1));
+  L.swin = L.starts + align256(sizeof(int32_t) * ((size_t)L.rcap + 1));
+  L.total = L.swin + align256(sizeof(int32_t) * (size_t)batch);
   return L;
 }
 
@@ -90,7 +91,7 @@ extern "C" int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indic
   return decode_plan_launch(kv_indptr, kv_indices, num_indices, kv_last_page_len, batch, num_ctas,
                             page_size, seg_cost_pages(num_kv_heads, head_dim, page_size), (int)L.rcap, (int32_t*)(ws + L.ghdr), (int32_t*)(ws + L.recs), (int32_t*)(ws + L.heads),
                             (int32_t*)(ws + L.rank), (int32_t*)(ws + L.bf), (int32_t*)(ws + L.starts),
-                            (hipStream_t)stream);
+                            (int32_t*)(ws + L.swin), (hipStream_t)stream);
 }
 
 extern "C" int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,

@@ -6,7 +6,7 @@
 // synchronises and the step's page table can be rebuilt on the device right before it (also
 // inside a captured graph).
 //
-// Steps (one workgroup of 1024 threads; every loop strides over the batch or the pages):
+// First phase (one workgroup of 1024 threads; every loop strides over the batch):
 //  1. total = min(kv_indptr[B], num_indices), first = kv_indptr[0]; the n = total - first pages
 //     are cut into R = max(min(num_ctas, n), ceil(n / kRangePages)) ranges.
 //  2. Sequence b owns pages [s0, s1) = kv_indptr[b .. b+1] clipped to [first, total).  An
@@ -14,8 +14,10 @@
 //     page are listed.
 //  3. Range starts cut the page list into R parts of equal weight (a page weighs 1, a sequence
 //     start seg_cost_pages); a range's first sequence is the one holding its first page.
-//  4. Sequence b is segment rank[b] - rank[first sequence of w] of every range w it touches.
-//  5. The page ids are copied range by range.
+//  4. Each sequence's first and last range are found in the LDS copy of the range starts.
+// Second phase (one workgroup per range, decode_plan_records_kernel): the range's sequences
+// become its segments (sequence b is segment rank[b] - rank[first sequence of the range]) and
+// its page ids are copied, coalesced.
 #include "attn_common.h"
 #include "decode_sched.h"
 #include "../../include/pagedkv.h"
@@ -36,6 +38,7 @@ struct PlanParams {
   int32_t* rank;    // [B] scratch
   int32_t* bf;      // [r_cap] scratch: first sequence of each range
   int32_t* starts;  // [r_cap + 1] scratch: first page-list position of each range
+  int32_t* swin;    // [B] scratch: first | last range << 16 of each sequence with pages
 };
 
 constexpr int kPlanThreads = 1024;
@@ -150,57 +153,86 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams P)
     }
     return lo;
   };
-  for (int w = tid; w < P.r_cap; w += kPlanThreads) {
-    int32_t* h = P.heads + (int64_t)w * kHeadWords;
-    h[kHdrLen] = w < R ? starts[w + 1] - starts[w] : 0;
-    h[kHdrNseg] = 0;
-    h[kHdrRanges] = R;
-  }
-  __syncthreads();
-
-  // ---- segments
+  // each sequence's first and last range (for the second phase's segment records)
   for (int b = tid; b < B; b += kPlanThreads) {
-    const int e1 = P.indptr[b + 1];
-    const int s0 = clip(P.indptr[b]), s1 = clip(e1);
-    if (s1 <= s0) continue;
-    const int wl = owner(s0), wh = owner(s1 - 1);
-    int nvl = P.last[b];
-    nvl = nvl < 0 ? 0 : (nvl > P.page_size ? P.page_size : nvl);
-    for (int w = wl; w <= wh; ++w) {
-      const int f = P.bf[w];
-      if (f < 0 || f > b || f >= B) continue;  // (only for a malformed, decreasing kv_indptr)
-      const int idx = P.rank[b] - P.rank[f];
-      const int rs = starts[w], re = starts[w + 1];
-      const int beg = (s0 > rs ? s0 : rs) - rs, end = (s1 < re ? s1 : re) - rs;
-      if (idx < 0 || idx >= kRangePages || end <= beg) continue;
-      // the segment's last page is the sequence's last page only if the page list was not cut
-      const int nv = (s1 == e1 && s1 <= re) ? nvl : P.page_size;
-      int32_t* rec = P.recs + (int64_t)w * kRecStride;
-      int4 sg;
-      sg.x = b;
-      sg.y = beg | (end << 16);
-      sg.z = nv;
-      sg.w = wl | (wh << 16);
-      *reinterpret_cast<int4*>(rec + kRecSegOff + 4 * idx) = sg;
-      int32_t* head = P.heads + (int64_t)w * kHeadWords;
-      if (idx < kHeadSegs) *reinterpret_cast<int4*>(head + kRecSegOff + 4 * idx) = sg;
-      atomicMax(head + kHdrNseg, idx + 1);
-    }
+    const int s0 = clip(P.indptr[b]), s1 = clip(P.indptr[b + 1]);
+    P.swin[b] = s1 > s0 ? owner(s0) | (owner(s1 - 1) << 16) : -1;
   }
-
-  // ---- page ids, range by range
-  for (int p = first + tid; p < total; p += kPlanThreads) {
-    const int w = owner(p), i = p - starts[w];
-    const int pid = P.indices[p];
-    P.recs[(int64_t)w * kRecStride + kRecPidOff + i] = pid;
-    if (i < kHeadPids) P.heads[(int64_t)w * kHeadWords + kHeadPidOff + i] = pid;
-  }
-  __syncthreads();
+  if (starts != P.starts)
+    for (int w = tid; w <= R; w += kPlanThreads) P.starts[w] = starts[w];
   if (tid == 0) {
     P.ghdr[kGhRanges] = R;
     P.ghdr[kGhEmpty] = s_nempty;
     P.ghdr[kGhTotal] = total;
     P.ghdr[kGhFirst] = first;
+  }
+}
+
+// Second phase: one workgroup per range slot w < r_cap writes the range's head and record (its
+// sequence segments and a copy of its page ids), all ranges at once.
+constexpr int kRecThreads = 256;
+
+__global__ __launch_bounds__(kRecThreads) void decode_plan_records_kernel(PlanParams P) {
+  __shared__ int s_nseg;
+  const int w = blockIdx.x, tid = threadIdx.x;
+  const int R = P.ghdr[kGhRanges];
+  int32_t* head = P.heads + (int64_t)w * kHeadWords;
+  int32_t* rec = P.recs + (int64_t)w * kRecStride;
+  if (w >= R) {  // unused slot: an empty header (R in every header bounds the decode's range loop)
+    if (tid == 0) {
+      head[kHdrLen] = 0;
+      head[kHdrNseg] = 0;
+      head[kHdrRanges] = R;
+    }
+    return;
+  }
+  const int B = P.batch, first = P.ghdr[kGhFirst], total = P.ghdr[kGhTotal];
+  const int rs = P.starts[w], re = P.starts[w + 1];
+  const int f = P.bf[w];
+  if (tid == 0) s_nseg = 0;
+  __syncthreads();
+  auto clip = [&](int64_t x) -> int { return (int)(x < first ? first : (x > total ? total : x)); };
+  // ---- segments: the sequences f, f + 1, ... that own pages in [rs, re)
+  if (f >= 0 && f < B) {
+    const int rf = P.rank[f];
+    for (int base = f; base < B; base += kRecThreads) {
+      const int b = base + tid;
+      bool past = true;
+      if (b < B) {
+        const int e1 = P.indptr[b + 1];
+        const int s0 = clip(P.indptr[b]), s1 = clip(e1);
+        past = s0 >= re;
+        if (!past && s1 > s0) {
+          const int idx = P.rank[b] - rf;
+          const int beg = (s0 > rs ? s0 : rs) - rs, end = (s1 < re ? s1 : re) - rs;
+          const int win = P.swin[b];
+          if (idx >= 0 && idx < kRangePages && end > beg && win >= 0) {
+            int nvl = P.last[b];
+            nvl = nvl < 0 ? 0 : (nvl > P.page_size ? P.page_size : nvl);
+            // the segment's last page is the sequence's last page only if the list was not cut
+            const int nv = (s1 == e1 && s1 <= re) ? nvl : P.page_size;
+            const int4 sg = make_int4(b, beg | (end << 16), nv, win);
+            *reinterpret_cast<int4*>(rec + kRecSegOff + 4 * idx) = sg;
+            if (idx < kHeadSegs) *reinterpret_cast<int4*>(head + kRecSegOff + 4 * idx) = sg;
+            atomicMax(&s_nseg, idx + 1);
+          }
+        }
+      }
+      if (__syncthreads_and(past ? 1 : 0)) break;  // (uniform: every thread sees the same result)
+    }
+  }
+  // ---- page ids
+  const int len = re - rs;
+  for (int i = tid; i < len; i += kRecThreads) {
+    const int pid = P.indices[rs + i];
+    rec[kRecPidOff + i] = pid;
+    if (i < kHeadPids) head[kHeadPidOff + i] = pid;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    head[kHdrLen] = len;
+    head[kHdrNseg] = s_nseg;
+    head[kHdrRanges] = R;
   }
 }
 
@@ -211,7 +243,7 @@ namespace pkv {
 int decode_plan_launch(const int32_t* indptr, const int32_t* indices, int64_t num_indices,
                        const int32_t* last, int batch, int num_ctas, int page_size, int seg_cost,
                        int r_cap, int32_t* ghdr, int32_t* recs, int32_t* heads, int32_t* rank,
-                       int32_t* bf, int32_t* starts, hipStream_t s) {
+                       int32_t* bf, int32_t* starts, int32_t* swin, hipStream_t s) {
   PlanParams P;
   P.indptr = indptr;
   P.last = last;
@@ -228,7 +260,9 @@ int decode_plan_launch(const int32_t* indptr, const int32_t* indices, int64_t nu
   P.rank = rank;
   P.bf = bf;
   P.starts = starts;
+  P.swin = swin;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, P);
+  hipLaunchKernelGGL(decode_plan_records_kernel, dim3(r_cap), dim3(kRecThreads), 0, s, P);
   return (int)hipGetLastError();
 }
 
