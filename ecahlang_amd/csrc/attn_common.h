@@ -1,14 +1,15 @@
 // Work partition and split-state merge shared by the paged decode kernels.
 //
 // Decode partitions the batch's concatenated page list (kv_indices[0 .. kv_indptr[B])) into
-// num_ctas equal page ranges, one per workgroup, independent of sequence boundaries: every
-// workgroup streams the same number of pages whatever the length mix.  A sequence cut by a
-// range boundary yields one partial softmax state per workgroup that touches it; those are
-// written to the workspace at slot (workgroup + sequence), which is unique because walking
-// the page list in order every new segment starts at a new workgroup, a new sequence, or
-// both.  The workgroup that arrives last for a sequence (an atomic counter per sequence)
-// merges the partials and resets the counter to zero, so the workspace needs zeroing once
-// (at plan time) and never inside a captured graph.
+// page ranges independent of sequence boundaries, so every workgroup streams about the same
+// number of pages whatever the length mix.  A sequence cut by range boundaries (or, with the
+// matrix-core kernel's schedule, also into shared-prefix chunks) yields one partial softmax
+// state per part; a sequence's parts occupy consecutive partial slots.  The vector kernel's
+// slot of (range w, sequence b) is w + b, which is unique because walking the page list in
+// order every new segment starts at a new range, a new sequence, or both; the plan assigns
+// the matrix-core kernel's slots.  The workgroup that arrives last for a sequence (an atomic
+// counter per sequence) merges the partials and resets the counter to zero, so the workspace
+// needs zeroing once (at plan time) and never inside a captured graph.
 #pragma once
 #include "common.h"
 
@@ -30,8 +31,9 @@ struct DecodeParams {
   void* out;
   int64_t o_sn, o_sh;
   int32_t* counters;           // [B]
-  float2* part_ml;             // [num_ctas + B][ml_stride] (running max, sum of exp)
-  float* part_o;               // [num_ctas + B][hq][D], normalised partial output
+  float2* part_ml;             // [slot_cap][ml_stride] (running max, sum of exp)
+  float* part_o;               // [slot_cap][hq][D], normalised partial output
+  int32_t slot_cap;            // partial slots in the workspace (>= num_ctas + B)
   int32_t num_ctas;
   int32_t q_vec;               // q rows / strides allow 16-byte loads
   int32_t o_vec;               // out rows / strides allow 8-byte stores
@@ -40,6 +42,7 @@ struct DecodeParams {
   const int32_t* sched;        // matrix-core kernel: the plan's range records (decode_sched.h)
   const int32_t* sched_hdr;    // ... and its global header
   const int32_t* sched_head;   // ... and the dense heads of its ranges
+  const int32_t* sched_pref;   // ... and its prefix item records
   int32_t r_cap;               // ranges the workspace holds
 };
 
@@ -126,7 +129,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 constexpr int kMergeRegs = 8;  // segments a merge folds from registers
 
-// Merges of the sequences queued in `list` (rows of sequence, w_lo, w_hi), all at once.
+// Merges of the sequences queued in `list` (rows of sequence, first slot, parts), all at once.
 // An item is 8 consecutive output dims of one head of one queued sequence; each thread takes
 // one item per round.  A wave loads only as many segments as the longest sequence among its
 // items has (a wave-uniform bound, so the loads need no divergent branch), and every load is
@@ -143,7 +146,7 @@ struct MergeItem {
     const bool real = item < nitems;
     const int it = real ? item : nitems - 1;
     const int i = it / per, r = it - i * per;
-    nseg = list[i][2] - list[i][1] + 1;
+    nseg = list[i][2];
     b = (real && nseg <= kMergeRegs) ? list[i][0] : -1;  // longer ones are merged from global memory
     h = r / (D / 8);
     d = (r - h * (D / 8)) * 8;
@@ -153,7 +156,7 @@ struct MergeItem {
   // from clamped indices.
   __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int i, int nsw) {
     const int ns = nseg < kMergeRegs ? nseg : kMergeRegs;
-    const int64_t slot0 = (int64_t)(list[i][1] + list[i][0]);
+    const int64_t slot0 = list[i][1];
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
       if (s < nsw) {
@@ -212,7 +215,7 @@ struct MergeItem {
 };
 
 template <typename T, int D>
-__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi);
+__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int slot_lo, int nseg);
 
 template <typename T, int D>
 __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*list)[3], int nm) {
@@ -239,15 +242,15 @@ __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*
   round(0);
   for (int base = nt; base < nitems; base += nt) round(base);
   for (int i = 0; i < nm; ++i)
-    if (list[i][2] - list[i][1] + 1 > kMergeRegs) merge_partials<T, D>(P, list[i][0], list[i][1], list[i][2]);
+    if (list[i][2] > kMergeRegs) merge_partials<T, D>(P, list[i][0], list[i][1], list[i][2]);
 }
 
-// Merge of sequence b's partials straight from global memory (any segment count).
+// Merge of sequence b's partials (slots slot_lo .. slot_lo + nseg - 1) straight from global
+// memory (any segment count).
 template <typename T, int D>
-__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int w_lo, int w_hi) {
+__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int slot_lo, int nseg) {
   T* out = reinterpret_cast<T*>(P.out);
-  const int nseg = w_hi - w_lo + 1;
-  const int64_t slot0 = (int64_t)(w_lo + b);
+  const int64_t slot0 = slot_lo;
   for (int idx = threadIdx.x; idx < P.hq * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
     const float2* ml = P.part_ml + slot0 * P.ml_stride + h;

@@ -6,10 +6,15 @@
 //   (ecahlang/main.py:203-204 construct, :341-347 / :444-455 plan, :68 run)
 //
 // Workspace (caller-owned bytes, 256-byte aligned regions; R = decode_ranges_cap ranges):
-//   [counters: int32 x batch] [part_ml: float2 x (R+batch) x ml_slot_stride(Hq)]
-//   [part_o: f32 x (R+batch) x Hq x D]  (each part_ml slot is whole 128-byte lines)
+//   [counters: int32 x batch]
 //   [schedule: global header + empty list (kGlobHdr + batch int32), R heads of kHeadWords
-//    int32, R records of kRecStride int32, plan scratch rank[batch], first-sequence[R] and range starts[R + 1]]
+//    int32, R range records of kRecStride int32, R prefix item records of kPrecStride int32,
+//    first-sequence[R], range starts[R + 1], non-empty ranges before[R + 1], plan scratch
+//    (decode_plan_scratch_words)]
+//   [part_ml: float2 x S x ml_slot_stride(Hq)] [part_o: f32 x S x Hq x D]
+// with S = R + batch partial slots, plus up to kMaxPrefixParts x batch more for shared-prefix
+// chunks when the workspace has room (each part_ml slot is whole 128-byte lines).  The layout
+// depends on the workspace size, so plan and run are given the same size.
 #include <mutex>
 #include "attn_common.h"
 #include "decode_sched.h"
@@ -18,10 +23,13 @@
 using namespace pkv;
 
 namespace pkv {
+int64_t decode_plan_scratch_words(int batch);
 int decode_plan_launch(const int32_t* indptr, const int32_t* indices, int64_t num_indices,
-                       const int32_t* last, int batch, int num_ctas, int page_size, int seg_cost,
-                       int r_cap, int32_t* ghdr, int32_t* recs, int32_t* heads, int32_t* rank,
-                       int32_t* bf, int32_t* starts, int32_t* swin, hipStream_t s);
+                       const int32_t* last, const int32_t* shared, int batch, int num_ctas,
+                       int page_size, int seg_cost, int group, int hkv, int cascade, int r_cap, int slot_cap,
+                       int32_t* ghdr, int32_t* recs, int32_t* heads, int32_t* precs, int32_t* bf,
+                       int32_t* starts, int32_t* nzb, int32_t* scratch, hipStream_t s);
+int decode_mfma_group(int d, int g, int hkv);
 }
 
 namespace {
@@ -29,24 +37,36 @@ namespace {
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t cnt, ml, o, ghdr, heads, recs, rank, bf, starts, swin, total;
-  int64_t rcap;
+  size_t cnt, ghdr, heads, recs, precs, bf, starts, nzb, scratch, ml, o, total;
+  int64_t rcap, slots;
 };
-inline WsLayout ws_layout(int batch, int hq, int d, int ctas, int64_t num_indices) {
+// Layout for a workspace of ws_bytes (< 0: the smallest one, without shared-prefix slots).
+inline WsLayout ws_layout(int batch, int hq, int d, int ctas, int64_t num_indices, int64_t ws_bytes = -1) {
   WsLayout L;
   L.rcap = decode_ranges_cap(ctas, num_indices);
-  size_t segs = (size_t)L.rcap + batch;
   L.cnt = 0;
-  L.ml = align256(sizeof(int32_t) * (size_t)batch);
-  L.o = L.ml + align256(sizeof(float) * 2 * segs * ml_slot_stride(hq));
-  L.ghdr = L.o + align256(sizeof(float) * segs * hq * d);
+  L.ghdr = align256(sizeof(int32_t) * (size_t)batch);
   L.heads = L.ghdr + align256(sizeof(int32_t) * ((size_t)kGlobHdr + batch));
   L.recs = L.heads + align256(sizeof(int32_t) * (size_t)L.rcap * kHeadWords);
-  L.rank = L.recs + align256(sizeof(int32_t) * (size_t)L.rcap * kRecStride);
-  L.bf = L.rank + align256(sizeof(int32_t) * (size_t)batch);
+  L.precs = L.recs + align256(sizeof(int32_t) * (size_t)L.rcap * kRecStride);
+  L.bf = L.precs + align256(sizeof(int32_t) * (size_t)L.rcap * kPrecStride);
   L.starts = L.bf + align256(sizeof(int32_t) * (size_t)L.rcap);
-  L.swin = L.starts + align256(sizeof(int32_t) * ((size_t)L.rcap + 1));
-  L.total = L.swin + align256(sizeof(int32_t) * (size_t)batch);
+  L.nzb = L.starts + align256(sizeof(int32_t) * ((size_t)L.rcap + 1));
+  L.scratch = L.nzb + align256(sizeof(int32_t) * ((size_t)L.rcap + 1));
+  L.ml = L.scratch + align256(sizeof(int32_t) * (size_t)decode_plan_scratch_words(batch));
+  const size_t ml_slot = sizeof(float) * 2 * ml_slot_stride(hq), o_slot = sizeof(float) * hq * d;
+  const int64_t base = L.rcap + batch;
+  int64_t extra = 0;
+  if (ws_bytes > 0) {
+    // (a 256-byte alignment pad per array)
+    const int64_t room = ws_bytes - (int64_t)L.ml - 512 - base * (int64_t)(ml_slot + o_slot);
+    extra = room > 0 ? room / (int64_t)(ml_slot + o_slot) : 0;
+    const int64_t cap = (int64_t)kMaxPrefixParts * batch;
+    extra = extra < cap ? extra : cap;
+  }
+  L.slots = base + extra;
+  L.o = L.ml + align256(ml_slot * (size_t)L.slots);
+  L.total = L.o + align256(o_slot * (size_t)L.slots);
   return L;
 }
 
@@ -54,9 +74,15 @@ __global__ void zero_i32_kernel(int32_t* p, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 
+// Sizes the schedule's words can hold: ranges and parts in 16 bits, sequences in 27, and the
+// partial outputs addressed with 32-bit byte offsets.
 bool ws_args_ok(int32_t batch, int32_t hq, int32_t d, int32_t ctas, int64_t num_indices) {
-  return batch >= 0 && hq > 0 && d > 0 && ctas > 0 && num_indices >= 0 &&
-         decode_ranges_cap(ctas, num_indices) + batch < (1 << 30);
+  if (!(batch >= 0 && batch < (1 << kSegBBits) && hq > 0 && d > 0 && ctas > 0 && num_indices >= 0))
+    return false;
+  const int64_t rcap = decode_ranges_cap(ctas, num_indices);
+  if (rcap > kMaxRanges) return false;
+  const int64_t slots = rcap + (int64_t)(1 + kMaxPrefixParts) * batch;
+  return slots * hq * d * (int64_t)sizeof(float) < ((int64_t)1 << 32);
 }
 
 }  // namespace
@@ -77,21 +103,27 @@ extern "C" int pkv_decode_workspace_init(void* workspace, int32_t batch, void* s
 }
 
 extern "C" int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indices,
-                               int64_t num_indices, const int32_t* kv_last_page_len, int32_t batch,
+                               int64_t num_indices, const int32_t* kv_last_page_len,
+                               const int32_t* kv_shared_pages, int32_t batch,
                                int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                               int32_t page_size, int32_t num_ctas, void* workspace,
-                               int64_t workspace_bytes, void* stream) {
+                               int32_t page_size, int32_t num_ctas, int32_t plan_flags,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch <= 0) return kOk;
   if (page_size <= 0) return kBadPageSize;
-  if (num_kv_heads <= 0) return kBadArg;
+  if (num_kv_heads <= 0 || num_qo_heads % num_kv_heads) return kBadArg;
   if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
-  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices);
+  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices, workspace_bytes);
   if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
   char* ws = (char*)workspace;
-  return decode_plan_launch(kv_indptr, kv_indices, num_indices, kv_last_page_len, batch, num_ctas,
-                            page_size, seg_cost_pages(num_kv_heads, head_dim, page_size), (int)L.rcap, (int32_t*)(ws + L.ghdr), (int32_t*)(ws + L.recs), (int32_t*)(ws + L.heads),
-                            (int32_t*)(ws + L.rank), (int32_t*)(ws + L.bf), (int32_t*)(ws + L.starts),
-                            (int32_t*)(ws + L.swin), (hipStream_t)stream);
+  const int group = decode_mfma_group(head_dim, num_qo_heads / num_kv_heads, num_kv_heads);
+  return decode_plan_launch(kv_indptr, kv_indices, num_indices, kv_last_page_len, kv_shared_pages,
+                            batch, num_ctas, page_size, seg_cost_pages(num_kv_heads, head_dim, page_size),
+                            group, num_kv_heads, (plan_flags & PKV_PLAN_CASCADE) ? 1 : 0, (int)L.rcap,
+                            (int)L.slots, (int32_t*)(ws + L.ghdr),
+                            (int32_t*)(ws + L.recs), (int32_t*)(ws + L.heads), (int32_t*)(ws + L.precs),
+                            (int32_t*)(ws + L.bf), (int32_t*)(ws + L.starts), (int32_t*)(ws + L.nzb),
+                            (int32_t*)(ws + L.scratch),
+                            (hipStream_t)stream);
 }
 
 extern "C" int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
@@ -117,7 +149,7 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return kBadHeadDim;
   if (num_indices < 0 || num_pages < 0) return kBadArg;
   if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
-  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices);
+  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices, workspace_bytes);
   if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
   DecodeParams P;
   P.q = q; P.q_sn = q_stride_n; P.q_sh = q_stride_h;
@@ -135,6 +167,8 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   P.sched_hdr = (const int32_t*)(ws + L.ghdr);
   P.sched = (const int32_t*)(ws + L.recs);
   P.sched_head = (const int32_t*)(ws + L.heads);
+  P.sched_pref = (const int32_t*)(ws + L.precs);
+  P.slot_cap = (int32_t)L.slots;
   P.r_cap = (int32_t)L.rcap;
   P.num_ctas = num_ctas;
   P.dynamic = (flags & PKV_DECODE_DYNAMIC) != 0;
@@ -215,8 +249,8 @@ extern "C" int pkv_batch_decode_noalloc(const void* q, int64_t q_stride_n, int64
   int flags = 0;
   if (page_size == 16 && num_qo_heads % num_kv_heads == 0 &&
       decode_mfma_supported(dtype, head_dim, num_qo_heads / num_kv_heads, num_kv_heads, batch)) {
-    if ((rc = pkv_decode_plan(kv_indptr, kv_indices, num_indices, kv_last_page_len, batch, num_qo_heads,
-                              num_kv_heads, head_dim, page_size, num_ctas, ws, ws_bytes, stream)))
+    if ((rc = pkv_decode_plan(kv_indptr, kv_indices, num_indices, kv_last_page_len, nullptr, batch, num_qo_heads,
+                              num_kv_heads, head_dim, page_size, num_ctas, 0, ws, ws_bytes, stream)))
       return rc;
     flags = PKV_DECODE_PLANNED;
   }

@@ -41,7 +41,7 @@ constexpr int W = 8;                // waves per workgroup
 constexpr int NT = W * 64;
 constexpr int kQArea = 8192;        // LDS bytes for query rows of the range's first segments
 constexpr int kSegLds = 64;         // segment records staged in LDS (more are read from memory)
-constexpr int kMaxSplit = 32;       // split segments whose arrival a workgroup defers
+constexpr int kMaxSplit = 64;       // split segments whose arrival a workgroup defers
 constexpr float kLazyMax = 8.f;     // a column's reference max moves only on jumps > 2^8
 
 template <int N>
@@ -97,18 +97,27 @@ __device__ __forceinline__ f4 fold_copies(int J, F&& copy) {
 }
 
 struct Seg {
-  int b, beg, end, nv, wlo, whi;
+  int b, beg, end, nv, slot0, part, nparts, np;
 };
-__device__ __forceinline__ Seg unpack_seg(int4 v, int len, int batch) {
+// A segment word (decode_sched.h), clamped so that a stale or malformed schedule cannot index
+// past the batch, the record or the partial slots.
+__device__ __forceinline__ Seg unpack_seg(int4 v, int len, int batch, int slot_cap) {
   Seg s;
-  s.b = v.x < 0 ? 0 : (v.x >= batch ? batch - 1 : v.x);
+  const int b = v.x & ((1 << kSegBBits) - 1);
+  s.b = b >= batch ? batch - 1 : b;
+  const int nv = (int)(((unsigned)v.x >> kSegBBits) & 31);
+  s.nv = nv > 16 ? 16 : nv;
+  s.np = (int)((unsigned)v.x >> (kSegBBits + 5));
   s.beg = v.y & 0xFFFF;
   s.end = (v.y >> 16) & 0xFFFF;
   s.end = s.end > len ? len : s.end;
   s.beg = s.beg > s.end ? s.end : s.beg;
-  s.nv = v.z < 0 ? 0 : (v.z > 16 ? 16 : v.z);
-  s.wlo = v.w & 0xFFFF;
-  s.whi = (v.w >> 16) & 0xFFFF;
+  s.nparts = ((v.w >> 16) & 0xFFFF) + 1;
+  s.nparts = s.nparts > slot_cap ? slot_cap : s.nparts;
+  s.slot0 = v.z < 0 ? 0 : (v.z > slot_cap - s.nparts ? slot_cap - s.nparts : v.z);
+  s.part = v.w & 0xFFFF;
+  s.part = s.part >= s.nparts ? s.nparts - 1 : s.part;
+  s.np = s.np >= s.nparts ? s.nparts - 1 : s.np;
   return s;
 }
 
@@ -137,7 +146,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   __shared__ int4 s_seg[kSegLds];
   __shared__ float2 s_ml[W][16];
   __shared__ f4 s_x[2][W][64];                // tile exchange at interior segment ends
-  __shared__ int s_split[kMaxSplit][3];       // deferred arrivals: sequence, w_lo, w_hi
+  __shared__ int s_split[kMaxSplit][4];       // deferred arrivals: sequence, first slot, parts, arrivals
   __shared__ int s_merge[kMaxSplit][3];       // merges owed after the arrivals
   __shared__ int s_nmerge;
   __shared__ int s_next[W];                   // PKV_DECODE_DYNAMIC: next page per head block
@@ -162,21 +171,33 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   const T* vc = reinterpret_cast<const T*>(P.v_cache);
   const T* qall = reinterpret_cast<const T*>(P.q);
   T* out = reinterpret_cast<T*>(P.out);
-  const int64_t rowstride = (int64_t)P.hkv * D;        // elements between token rows
+  const int rowstride32 = P.hkv * D;                   // elements between token rows
   const int64_t hboff = (int64_t)hb * HB * D;
 
-  // copy of unit (page pg) rows into a staged tile; `x` is the row swizzle
-  auto issue_tile = [&](const T* base, int64_t pg, char* dst, bool isv) __attribute__((always_inline)) {
+  // copy of unit (page pg, head block at element offset hoff) rows into a staged tile, rows
+  // swizzled; streamed (nt) or, for pages other workgroups read too, cached
+  auto issue_tile = [&](const T* base, int64_t pg, char* dst, bool isv, int64_t hoff = -1,
+                        bool nt = true) __attribute__((always_inline)) {
+    if (hoff < 0) hoff = hboff;
+    const T* pbase = base + pg * P.page_stride + hoff;  // (row offsets fit in 32 bits)
+    // The per-copy offsets are recomputed at every call (a few VALU operations): hoisted out of
+    // the page loop they would hold 2 * NI registers for the whole loop.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int t = i * RPI + lane / CPR, pos = lane % CPR;
+      const int t = i * RPI + ln / CPR, pos = ln % CPR;
       const int col = pos ^ (isv ? vx<RB>(t) : kx<RB>(t));
-      dma16_nt(base + pg * P.page_stride + t * rowstride + hboff + 8 * col, dst + i * 1024);
+      const T* src = pbase + (t * rowstride32 + 8 * col);
+      if (nt) dma16_nt(src, dst + i * 1024); else dma16(src, dst + i * 1024);
     }
   };
   auto page_ok = [&](int pid) __attribute__((always_inline)) -> bool {
     return pid >= 0 && (int64_t)pid < P.num_pages;
   };
+  // a range record's page id word: the page, and whether other sequences read it too
+  auto pid_page = [](int raw) __attribute__((always_inline)) -> int { return raw < 0 ? raw : raw & ~kPidShared; };
+  auto pid_cached = [](int raw) __attribute__((always_inline)) -> bool { return raw >= 0 && (raw & kPidShared); };
 
   const int N0 = P.num_ctas;
   // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each XCD a
@@ -195,10 +216,10 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       int sb = 0, lo = 0, hi = 0, last = 0;
       if (lane < nsplit) {
         sb = s_split[lane][0];
-        lo = s_split[lane][1];
-        hi = s_split[lane][2];
+        lo = s_split[lane][1];  // first slot
+        hi = s_split[lane][2];  // parts
         const int old = atomicAdd(&P.counters[sb], 1);
-        last = old == hi - lo;
+        last = old == s_split[lane][3] - 1;
         if (last) __hip_atomic_store(&P.counters[sb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       const uint64_t bal = __ballot(last);
@@ -222,6 +243,214 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     nsplit = 0;
   };
 
+  // ---- prefix item (decode_sched.h): G sequences x one chunk of pages x one KV head, all
+  // shared.  The head's K and V rows of the chunk's pages (tiles of 16 rows of D elements)
+  // stream through a ring of NS = W * HB page slots in the unit buffers: page p is copied by
+  // wave p % W into slot p % NS with the cached policy (every group of the run reads the chunk),
+  // and a wave may have NS / W pages in flight.  The pages are processed two at a time, with
+  // one barrier per step that publishes the step's pages (their copiers waited for them) and
+  // frees the slots of the previous step for the pages NS ahead.
+  // Every wave attends head h: a column is (sequence, query head of h), 16 / g sequences per
+  // 16-column block, and a wave takes NB = 2 blocks (1 when that would exceed kMaxGroup), so
+  // each K/V fragment read from LDS feeds NB products; G = W * NB * (16 / g).
+  constexpr int RB1 = D * 2, CPR1 = RB1 / 16, RPI1 = 64 / CPR1, NI1 = 16 / RPI1, TILE1 = 16 * RB1;
+  constexpr int NSP = W * 2 * TILE / (2 * TILE1);      // ring slots (pages)
+  static_assert(NSP >= 4 && NSP % W == 0 && NSP / W <= 4, "prefix ring");
+  const float scale = P.scale_log2;
+  auto prefix_item = [&](int w) __attribute__((always_inline)) {
+    const int32_t* pr = P.sched_pref + (int64_t)w * kPrecStride;
+    const int hv2 = pr[lane];
+    int plen = __builtin_amdgcn_readlane(hv2, kHdrLen);
+    plen = plen < 0 ? 0 : (plen > kRangePages ? kRangePages : plen);
+    int pn = __builtin_amdgcn_readlane(hv2, kHdrNseg);
+    pn = pn < 0 ? 0 : (pn > kMaxGroup ? kMaxGroup : pn);
+    int hd = __builtin_amdgcn_readlane(hv2, kHdrHead);
+    hd = hd < 0 ? 0 : (hd >= P.hkv ? P.hkv - 1 : hd);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (nsplit + kMaxGroup > kMaxSplit) flush_splits(true);  // room for this item's arrivals
+    lds_barrier();  // the previous readers of s_pid and of the unit buffers are done
+    for (int k = wave; k < (plen + 255) / 256; k += W)
+      dma16(pr + kPrecPidOff + 256 * k + 4 * lane, reinterpret_cast<const char*>(s_pid + 256 * k));
+    // my columns and their sequences (segment e = (NB wave + k) * spb + column / g)
+    const int spb = 16 / g, sib = lr / g, gi = lr - sib * g;
+    const int nb = W * 2 * spb <= kMaxGroup ? 2 : 1;
+    const int qhd = hd * g + gi;                        // query head of my column
+    Seg sgk[2];
+    bool ok[2];
+    uint4 qk2[2][KSH];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = (nb * wave + k) * spb + sib;
+      ok[k] = k < nb && sib < spb && e < pn;
+      const int4 v = *reinterpret_cast<const int4*>(pr + kPrecSegOff + 4 * (ok[k] ? e : 0));
+      sgk[k] = unpack_seg(v, plen, B, P.slot_cap);
+      const T* src = qall + (int64_t)sgk[k].b * P.q_sn + (int64_t)qhd * P.q_sh + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < KSH; ++s)
+        qk2[k][s] = ok[k] ? *reinterpret_cast<const uint4*>(src + 32 * s) : make_uint4(0, 0, 0, 0);
+    }
+    f4 po[2][MT];
+    float pm[2], pl[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) po[k][mt] = f4{0.f, 0.f, 0.f, 0.f};
+      pm[k] = -INFINITY;
+      pl[k] = 0.f;
+    }
+    const bool any = __ballot(ok[0] || ok[1]) != 0;
+    // the page ids and the query rows have landed; a wait the compiler sees, so it inserts none
+    // of its own for the query registers inside the page loop (one would drain the page copies)
+    wait_stores();
+    lds_barrier();
+    // one head's K and V rows of page p into its ring slot
+    const int64_t hoff = (int64_t)hd * D;
+    auto issue_page = [&](int p) __attribute__((always_inline)) {
+      const int pid = __builtin_amdgcn_readfirstlane(s_pid[p]);
+      const int64_t pg = page_ok(pid) ? pid : 0;
+      char* dst = smem + (p % NSP) * 2 * TILE1;
+      const T* kb = kc + pg * P.page_stride + hoff;
+      const T* vb = vc + pg * P.page_stride + hoff;
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+#pragma unroll
+        for (int i = 0; i < NI1; ++i) {
+          const int t = i * RPI1 + ln / CPR1, pos = ln % CPR1;
+          const int col = pos ^ (x ? vx<RB1>(t) : kx<RB1>(t));
+          dma16((x ? vb : kb) + (t * rowstride32 + 8 * col), dst + x * TILE1 + i * 1024);
+        }
+      }
+    };
+    constexpr int step = 2;
+    for (int p = wave; p < NSP - step && p < plen; p += W) issue_page(p);
+    for (int p0 = 0; p0 < plen; p0 += step) {
+      const int np2 = min(step, plen - p0);            // pages this step (1 or 2)
+      // the copier of each of this step's pages waits for it; its later pages (p + W, ...)
+      // already issued stay in flight (copies complete in issue order)
+      const int issued = min(plen, p0 + NSP - step);
+      const int mine_p = wave == p0 % W ? p0 : ((np2 == 2 && wave == (p0 + 1) % W) ? p0 + 1 : -1);
+      if (mine_p >= 0) {
+        const int newer = mine_p + W < issued ? (issued - 1 - mine_p) / W : 0;
+        if (newer == 0) wait_vm<0>();
+        else if (newer == 1) wait_vm<2 * NI1>();
+        else if (newer == 2) wait_vm<4 * NI1>();
+        else wait_vm<6 * NI1>();
+      }
+      lds_barrier();
+      for (int q = p0 + NSP - step; q < p0 + NSP && q < plen; ++q)
+        if (wave == q % W) issue_page(q);
+      const int pid0 = __builtin_amdgcn_readfirstlane(s_pid[p0]);
+      const int pid1 = np2 == 2 ? __builtin_amdgcn_readfirstlane(s_pid[p0 + 1]) : pid0;
+      const bool v0 = page_ok(pid0), v1 = np2 == 2 && page_ok(pid1);
+      if (!any) continue;
+      // Straight-line step (no branch between the LDS reads and their products, so they can
+      // all be in flight together): both pages and both blocks always; the second page's slot
+      // may hold stale rows (a lone last page) and a page outside the pool holds page 0's rows,
+      // so their scores are replaced by -inf and their V fragments by zeros, by selects.
+      const char* kb0 = smem + (p0 % NSP) * 2 * TILE1;
+      const char* kb1 = smem + ((p0 + 1) % NSP) * 2 * TILE1;
+      // lane-derived LDS offsets are recomputed here, not kept from the kernel's start (kept,
+      // they are spilled, and their reloads would wait for every page copy in flight)
+      int l2 = lane;
+      asm volatile("" : "+v"(l2));
+      const int lr2 = l2 & 15, lg2 = l2 >> 4;
+      uint4 ka[2][KSH];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const char* krow = (x ? kb1 : kb0) + lr2 * RB1;
+#pragma unroll
+        for (int s = 0; s < KSH; ++s)
+          ka[x][s] = *reinterpret_cast<const uint4*>(krow + (((4 * s + lg2) ^ kx<RB1>(lr2)) << 4));
+      }
+      f4 sa[2][2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          sa[x][k] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < KSH; ++s) sa[x][k] = Mma<T>::qk(ka[x][s], qk2[k][s], sa[x][k]);
+        }
+      }
+      // V^T fragments of both pages (read now, used after the softmax)
+      const int tr_row = 4 * lg2 + (lr2 >> 2);
+      const char* vb0 = kb0 + TILE1 + tr_row * RB1 + (lr2 & 1) * 8;
+      const char* vb1 = kb1 + TILE1 + tr_row * RB1 + (lr2 & 1) * 8;
+      uint4 va[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int c = (2 * mt + ((lr2 & 3) >> 1)) ^ vx<RB1>(tr_row);
+        const uint2 a0 = lds_read_tr16(vb0 + (c << 4));
+        const uint2 a1 = lds_read_tr16(vb1 + (c << 4));
+        va[mt] = make_uint4(v0 ? a0.x : 0u, v0 ? a0.y : 0u, v1 ? a1.x : 0u, v1 ? a1.y : 0u);
+      }
+      // online softmax per block over the step's 16 or 32 tokens (every chunk page is full)
+      uint4 pb[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        float sv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sv[i] = v0 ? sa[0][k][i] : -INFINITY;
+          sv[4 + i] = v1 ? sa[1][k][i] : -INFINITY;
+        }
+        float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                           fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float cms = cmax * scale;
+        const bool grow = cms > pm[k] + kLazyMax;
+        if (__ballot(grow)) {
+          const float mnew = grow ? cms : pm[k];
+          const float alpha = __builtin_amdgcn_exp2f(pm[k] - mnew);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) po[k][mt] *= alpha;
+          pl[k] *= alpha;
+          pm[k] = mnew;
+        }
+        const float nmu = pm[k] == -INFINITY ? 0.f : -pm[k];
+        float e8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e8[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], scale, nmu));
+        pl[k] += ((e8[0] + e8[1]) + (e8[2] + e8[3])) + ((e8[4] + e8[5]) + (e8[6] + e8[7]));
+        pb[k] = make_uint4(Mma<T>::pack(e8[0], e8[1]), Mma<T>::pack(e8[2], e8[3]),
+                           Mma<T>::pack(e8[4], e8[5]), Mma<T>::pack(e8[6], e8[7]));
+      }
+      // O^T += V^T P over the step's tokens: reduction slots 0-3 the first page, 4-7 the second
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        po[0][mt] = Mma<T>::qk(va[mt], pb[0], po[0][mt]);
+        po[1][mt] = Mma<T>::qk(va[mt], pb[1], po[1][mt]);
+      }
+    }
+    // each block's columns: this head's share of one part of each of its sequences
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      float ltot = pl[k] + __shfl_xor(pl[k], 16, 64);
+      ltot += __shfl_xor(ltot, 32, 64);
+      if (ok[k]) {
+        const int64_t slot = (int64_t)sgk[k].slot0 + sgk[k].part;
+        const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+        const int64_t sidx = slot * P.hq + qhd;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), po[k][mt] * inv);
+        if (lg == 0) store_partial_ml(P, slot, qhd, pm[k], ltot);
+        if (gi == 0 && lg == 0) {
+          const int e = (nb * wave + k) * spb + sib;
+          s_split[nsplit + e][0] = sgk[k].b;
+          s_split[nsplit + e][1] = sgk[k].slot0;
+          s_split[nsplit + e][2] = sgk[k].nparts;
+          s_split[nsplit + e][3] = sgk[k].nparts + sgk[k].np * (P.hkv - 1);
+        }
+      }
+    }
+    nsplit += pn;
+    lds_barrier();  // every wave is done with the ring; the arrivals are queued
+  };
+
   int rmax = P.r_cap;  // ranges of this plan (from the first record; never past the workspace)
   for (int w = w0; w < rmax; w += N0) {
     const int32_t* rec = P.sched + (int64_t)w * kRecStride;
@@ -238,6 +467,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     nseg = nseg < 0 ? 0 : (nseg > len ? len : nseg);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // round 1 complete (compiler-visible vmcnt(0))
     if (w >= rmax) break;
+    if (__builtin_amdgcn_readlane(hv, kHdrPrefix)) prefix_item(w);
     if (nseg == 0) continue;
     // segment s < kHeadSegs from the round-1 registers
     auto seg_reg = [&](int s) __attribute__((always_inline)) -> int4 {
@@ -268,7 +498,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         int4 sv = seg_reg(0);
 #pragma unroll
         for (int x = 1; x < 4; ++x) sv = s == x ? seg_reg(x) : sv;
-        const int b = unpack_seg(sv, len, B).b;
+        const int b = unpack_seg(sv, len, B, P.slot_cap).b;
         dma16(qall + (int64_t)b * P.q_sn + (int64_t)h * P.q_sh + 8 * dc, qarea + 1024 * i);
       }
     }
@@ -277,10 +507,11 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     int cpid = 0;
     bool have = pi < len;
     if (have) {
-      cpid = __builtin_amdgcn_readlane(pv, pi);
+      const int raw = __builtin_amdgcn_readlane(pv, pi);
+      cpid = pid_page(raw);
       const int64_t pg = page_ok(cpid) ? cpid : 0;
-      issue_tile(kc, pg, kbuf, false);
-      issue_tile(vc, pg, vbuf, true);
+      issue_tile(kc, pg, kbuf, false, -1, !pid_cached(raw));
+      issue_tile(vc, pg, vbuf, true, -1, !pid_cached(raw));
     }
     if (have) wait_vm<2 * NI>(); else wait_vm<0>();
     lds_barrier();
@@ -299,12 +530,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         v = make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                       __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
       }
-      Seg sgv = unpack_seg(v, len, B);
-      // (a valid plan has w_lo <= w <= w_hi < R; clamped so a stale one cannot index past the
-      // partial slots)
-      sgv.whi = sgv.whi < rmax ? sgv.whi : rmax - 1;
-      sgv.wlo = sgv.wlo < sgv.whi ? sgv.wlo : sgv.whi;
-      return sgv;
+      return unpack_seg(v, len, B, P.slot_cap);
     };
     uint4 qop[KS];
     f4 o[MT];
@@ -333,7 +559,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     auto end_segment = [&]() __attribute__((always_inline)) {
       float ltot = lsum + __shfl_xor(lsum, 16, 64);
       ltot += __shfl_xor(ltot, 32, 64);
-      const bool whole = sg.wlo == sg.whi;
+      const bool whole = sg.nparts == 1;
       float M = m, L = ltot;
       if (J > 1) {
         // (every read of the J copies is issued at once: slots past J repeat slot 0 and are
@@ -389,8 +615,9 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       }
       if (!whole && threadIdx.x == 0) {
         s_split[nsplit][0] = sg.b;
-        s_split[nsplit][1] = sg.wlo;
-        s_split[nsplit][2] = sg.whi;
+        s_split[nsplit][1] = sg.slot0;
+        s_split[nsplit][2] = sg.nparts;
+        s_split[nsplit][3] = sg.nparts + sg.np * (P.hkv - 1);
       }
       if (colv) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -408,7 +635,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
             }
           }
         } else {
-          const int64_t slot = (int64_t)w + sg.b, sidx = slot * P.hq + qh;
+          const int64_t slot = (int64_t)sg.slot0 + sg.part, sidx = slot * P.hq + qh;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             if (mt % J != j) continue;
@@ -424,7 +651,6 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     };
 
     start_segment();
-    const float scale = P.scale_log2;
     while (have) {
       while (si < nseg && pi >= sg.end) end_segment();
       if (si >= nseg) {  // (a page no segment covers: only for a malformed schedule)
@@ -449,10 +675,12 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         nxt = __builtin_amdgcn_readfirstlane(v);
       }
       const bool more = nxt < len;
-      int npid = 0;
-      if (more) npid = __builtin_amdgcn_readfirstlane(s_pid[nxt]);
+      int nraw = 0;
+      if (more) nraw = __builtin_amdgcn_readfirstlane(s_pid[nxt]);
+      const int npid = pid_page(nraw);
+      const bool nnt = !pid_cached(nraw);
       wait_lgkm0();  // the K tile has been read: it can be refilled
-      if (more) issue_tile(kc, page_ok(npid) ? npid : 0, kbuf, false);
+      if (more) issue_tile(kc, page_ok(npid) ? npid : 0, kbuf, false, -1, nnt);
       // softmax over the unit's 16 tokens (only a sequence's last page is partial)
       int nv = pi == sg.end - 1 ? sg.nv : 16;
       nv = page_ok(cpid) ? nv : 0;
@@ -509,7 +737,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         }
       }
       wait_lgkm0();  // the V tile has been read: it can be refilled
-      if (more) issue_tile(vc, page_ok(npid) ? npid : 0, vbuf, true);
+      if (more) issue_tile(vc, page_ok(npid) ? npid : 0, vbuf, true, -1, nnt);
       pi = nxt;
       cpid = npid;
       have = more;
@@ -559,6 +787,15 @@ bool decode_mfma_supported(int dtype, int d, int g, int hkv, int batch) {
   if (!((dtype == kF16 || dtype == kBF16) && (d == 64 || d == 128) && g >= 1 && g <= 16 && hkv >= 1))
     return false;
   return hkv / head_block(d, g, hkv) <= W;
+}
+
+// Sequences that share one prefix item, G = W * NB * (16 / g) (NB = 2 blocks per wave, 1 when
+// that would exceed kMaxGroup), or 0 when the shape cannot group.
+int decode_mfma_group(int d, int g, int hkv) {
+  if (!((d == 64 || d == 128) && g >= 1 && g <= 16 && hkv >= 1)) return 0;
+  const int spb = 16 / g, nb = W * 2 * spb <= kMaxGroup ? 2 : 1;
+  const int G = W * nb * spb;
+  return G <= kMaxGroup ? G : 0;
 }
 
 int decode_mfma_dispatch(const DecodeParams& P, int dtype, int d, hipStream_t s) {

@@ -1,24 +1,49 @@
 // Decode schedule: the per-plan work list the matrix-core decode kernel reads.
 //
-// pkv_decode_plan (BatchDecodeWithPagedKVCacheWrapper.plan) enqueues decode_plan_kernel, which
-// cuts the batch's page list (kv_indices[kv_indptr[0] .. kv_indptr[B]), clipped to num_indices)
-// into R equal ranges and writes one fixed-size record per range into the workspace:
-//   header   [len, nseg, R, 0, ...]                      kRecHdr int32 (in the range's head)
-//   segments nseg x {b, beg | end << 16, nv, w_lo | w_hi << 16}
+// pkv_decode_plan (BatchDecodeWithPagedKVCacheWrapper.plan) builds it on the device.
+//
+// Suffix ranges.  The batch's page list (kv_indices[kv_indptr[0] .. kv_indptr[B]), clipped to
+// num_indices), minus the shared prefix pages described below, is cut into R ranges of equal
+// weight; each range gets one fixed-size record:
+//   header   [len, nseg, R, prefix, ...]                 kRecHdr int32 (in the range's head)
+//   segments nseg x int4 {b | nv << 22 | np << 27, beg | end << 16, slot0,
+//                         part | (nparts - 1) << 16}
 //            one per sequence with pages in the range: range pages [beg, end) are sequence
 //            b's, nv is the valid token count of the segment's last page (16 unless that page
-//            is the sequence's last), and the sequence spans ranges w_lo .. w_hi
-//   page ids the range's len page ids, copied from kv_indices
+//            is the sequence's last).  The sequence's softmax state is cut into nparts parts
+//            whose partials live in slots slot0 .. slot0 + nparts - 1; this segment is part
+//            `part` (nparts == 1: the segment is the whole sequence and writes the output).
+//            The first np parts are shared-prefix chunks, each written by Hkv prefix items
+//            (one per KV head), so the sequence's merge waits for nparts + np (Hkv - 1)
+//            arrivals.
+//   page ids the range's len page ids, each with kPidShared set when other sequences of the
+//            batch read the same page (then it is copied with the cached policy, so the
+//            readers after the first find it in L2; other pages stream past the caches), and -1
+//            for an id that cannot be a page (negative, or kPidShared and above)
 // so a decode workgroup learns everything it needs to start streaming pages from one record,
-// in one memory round trip, instead of searching kv_indptr first.  The decode launches of all
-// layers of a step share the plan.  A global header before the records holds R and the
-// sequences that own no page (their output rows are zeros).
+// in one memory round trip.  The decode launches of all layers of a step share the plan.  A
+// global header before the records holds R and the sequences that own no page (their output
+// rows are zeros).
+//
+// Shared prefixes.  With the optional kv_shared_pages hint (for each sequence b >= 1, how many of
+// its leading pages are the same pages as sequence b - 1's), the common prefix of a run of
+// consecutive sequences that share at least kPrefixMinPages pages is marked kPidShared.
+// Cascade (PKV_PLAN_CASCADE): the common prefix is instead read once per group of G sequences
+// rather than once per sequence: the prefix is cut into chunks, and a prefix item
+// (G sequences x one chunk x one KV head) is carried by one range.  Its record:
+//   header   [len, nseg, head]                           (nseg <= G <= kMaxGroup sequences)
+//   segments nseg x int4, as above (beg = 0, end = len, part = the chunk's index)
+//   page ids the chunk's len page ids
+// The workgroup that owns the range streams the head's rows of each chunk page into LDS once,
+// and its waves attend all G sequences to them.  (One head per item: a workgroup's own load
+// rate is what bounds an item, so an item reads as little as possible for the most sequences.)  A grouped sequence's parts are its prefix chunks followed
+// by its suffix ranges, merged like any split sequence.
 #pragma once
 #include <stdint.h>
 
 namespace pkv {
 
-constexpr int kRangePages = 512;                       // pages per range at most
+constexpr int kRangePages = 512;                       // pages per range (and per chunk) at most
 // Weight of a sequence start when the plan cuts the page list, in K/V bytes: a range that holds
 // one more segment synchronises its waves mid-range to combine their states, which costs about
 // as long as a workgroup takes to stream this many bytes (measured at Qwen2.5-3B B=64: 12
@@ -33,7 +58,7 @@ constexpr int kRecHdr = 16;                            // header words
 constexpr int kRecSegOff = kRecHdr;                    // segment records (4 words each)
 constexpr int kRecPidOff = kRecSegOff + 4 * kRangePages;
 constexpr int kRecStride = (kRecPidOff + kRangePages + 63) / 64 * 64;  // words, 256-byte multiple
-enum RecHdr { kHdrLen = 0, kHdrNseg = 1, kHdrRanges = 2 };
+enum RecHdr { kHdrLen = 0, kHdrNseg = 1, kHdrRanges = 2, kHdrPrefix = 3, kHdrHead = 2 };
 // Head of each range: the header, its first kHeadSegs segments and first kHeadPids page ids,
 // 512 bytes per range in one dense array, which is all a decode workgroup reads before its
 // first page copies (one contiguous area for every workgroup's first read).
@@ -42,7 +67,28 @@ constexpr int kHeadSegs = 12;                          // words 16 .. 63
 constexpr int kHeadPidOff = 64;
 constexpr int kHeadPids = 64;                          // words 64 .. 127
 constexpr int kGlobHdr = 16;                           // global header words (then the empty list)
-enum GlobHdr { kGhRanges = 0, kGhEmpty = 1, kGhTotal = 2, kGhFirst = 3 };
+constexpr int kPidShared = 1 << 30;                    // page id flag: read by several sequences
+enum GlobHdr { kGhRanges = 0, kGhEmpty = 1, kGhTotal = 2, kGhFirst = 3, kGhItems = 4, kGhSuffix = 5, kGhRuns = 6 };
+
+// Prefix item records (indexed by the range that carries the item).
+constexpr int kMaxGroup = 32;                          // sequences per prefix item at most
+constexpr int kPrecSegOff = 16;                        // <= kMaxGroup segments: words 16 .. 143
+constexpr int kPrecPidOff = 256;
+constexpr int kPrecStride = kPrecPidOff + kRangePages; // words, 256-byte multiple
+constexpr int kPrefixMinPages = 16;                    // shorter shared prefixes are not grouped
+constexpr int kPrefixChunkMin = 32;                    // pages per chunk, unless that makes too many
+constexpr int kMaxPrefixParts = 4;                     // chunks per prefix (more only past 4 x 512 pages)
+constexpr int kMaxPrefixNp = 31;                       // chunks per prefix at most (5 bits)
+// A prefix item's weight when the plan balances the ranges, in streamed pages: the bytes it
+// reads (one head's rows of C pages) times kPrefixCostNum / kPrefixCostDen.
+constexpr int kPrefixCostNum = 1, kPrefixCostDen = 1;
+
+// Segment word packing.
+constexpr int kSegBBits = 22;
+__host__ __device__ inline int seg_pack_b(int b, int nv, int np) {
+  return (int)((unsigned)b | ((unsigned)nv << kSegBBits) | ((unsigned)np << (kSegBBits + 5)));
+}
+__host__ __device__ inline int seg_pack_part(int part, int nparts) { return part | ((nparts - 1) << 16); }
 
 // Ranges a plan may use: one per workgroup, more when that would put over kRangePages pages in
 // one range (num_indices bounds the page count).
@@ -50,5 +96,6 @@ inline int64_t decode_ranges_cap(int num_ctas, int64_t num_indices) {
   const int64_t need = (num_indices + kRangePages - 1) / kRangePages;
   return need > num_ctas ? need : num_ctas;
 }
+constexpr int64_t kMaxRanges = 60000;                  // segment words hold part / nparts in 16 bits
 
 }  // namespace pkv

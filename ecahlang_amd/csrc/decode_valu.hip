@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams P) {
       }
       __syncthreads();
     }
-    if (!whole && arrive_last(P, b, w_hi - w_lo + 1, &flag)) merge_partials<T, D>(P, b, w_lo, w_hi);
+    if (!whole && arrive_last(P, b, w_hi - w_lo + 1, &flag)) merge_partials<T, D>(P, b, w_lo + b, w_hi - w_lo + 1);
     p = seg_end;
     ++b;
     while (b < P.batch && P.indptr[b + 1] <= p) ++b;

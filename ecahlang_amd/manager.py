@@ -231,6 +231,9 @@ class AutoKVCacheManager:
         self._cg_append_indptr: dict = {}
         self._cg_meta: dict = {}  # bucket -> [desc | indptr | last_page_len | positions] (the three are views)
         self._cg_slots: dict = {}  # bucket -> each row's append slot, page * block_size + position % block_size
+        # bucket -> for each row, the leading pages it shares with the row before it (the
+        # decode plan's kv_shared_pages)
+        self._cg_kv_shared: dict = {}
         # The pool's initial state (free stack, page table, cache) is written on the current
         # stream; a caller may go on to drive the pool from another stream, so it is complete
         # before the constructor returns.
@@ -261,8 +264,8 @@ class AutoKVCacheManager:
         """The gather's input for the sequences ``ids`` followed by ``bucket - len(ids)``
         padding rows (one padding page each, last_page_len 1, position 0), staged in one host
         array: [desc (4 per row) | kv_indptr (rows + 1) | kv_last_page_len (rows)] plus
-        [positions (rows)] (each row's newest token) when asked.  Returns (slot, array, rows,
-        pages)."""
+        [positions (rows) | shared (rows)] (each row's newest token, and how many leading pages
+        it shares with the row before it) when asked.  Returns (slot, array, rows, pages)."""
         r = len(ids)
         b = max(bucket, r)
         if b - r > self._n_padding:
@@ -270,7 +273,7 @@ class AutoKVCacheManager:
         slots = np.fromiter(map(self.batch_to_seq_len.__getitem__, ids), np.int32, r)
         npages = np.fromiter(map(self._npages.__getitem__, ids), np.int32, r)
         plen = np.fromiter(map(self.batch_to_page_lengths.__getitem__, ids), np.int32, r)
-        slot, out = self._staging.host((7 if positions else 6) * b + 1)
+        slot, out = self._staging.host((8 if positions else 6) * b + 1)
         desc = out[: 4 * b].reshape(b, 4)
         desc[:r, 0] = slots
         desc[r:, 0] = self._rows - 1
@@ -290,6 +293,14 @@ class AutoKVCacheManager:
             np.multiply(npages - 1, self.block_size, out=pos[:r])
             pos[:r] += plen - 1
             pos[r:] = 0
+            shared = out[7 * b + 1: 8 * b + 1]
+            shared[:] = 0
+            if self._shared and r > 1:
+                sh = [self._shared.get(i) for i in ids]
+                for k in range(1, r):
+                    a, c = sh[k - 1], sh[k]
+                    if a is not None and c is not None and a[0] == c[0]:
+                        shared[k] = min(a[1], c[1])
         return slot, out, b, int(indptr[-1])
 
     def _gather(self, slot: int, staged: np.ndarray, b: int, pages: int, out_indices: torch.Tensor,
@@ -481,14 +492,15 @@ class AutoKVCacheManager:
         for bs in bucket_sizes:
             self._cg_kv_indices[bs] = torch.zeros(max(self.max_blocks, max_indices or 0), dtype=torch.int32,
                                                   device=dev)
-            # indptr, last_page_len and positions are views of one block laid out as the
-            # metadata build stages them, so one host copy fills all three
-            meta = torch.zeros(7 * bs + 1, dtype=torch.int32, device=dev)
+            # indptr, last_page_len, positions and the shared-prefix hint are views of one block
+            # laid out as the metadata build stages them, so one host copy fills all four
+            meta = torch.zeros(8 * bs + 1, dtype=torch.int32, device=dev)
             self._cg_meta[bs] = meta
             self._cg_kv_indptr[bs] = meta[4 * bs: 5 * bs + 1]
             self._cg_kv_last_page_len[bs] = meta[5 * bs + 1: 6 * bs + 1]
             self._cg_batch_indices[bs] = torch.arange(bs, dtype=torch.int32, device=dev)
             self._cg_positions[bs] = meta[6 * bs + 1: 7 * bs + 1]
+            self._cg_kv_shared[bs] = meta[7 * bs + 1: 8 * bs + 1]
             self._cg_slots[bs] = torch.full((bs,), -1, dtype=torch.int32, device=dev)
             self._cg_append_indptr[bs] = torch.arange(bs + 1, dtype=torch.int32, device=dev)
             self._cg_temperature[bs] = torch.ones(bs, 1, dtype=torch.float32, device=dev)
@@ -498,14 +510,16 @@ class AutoKVCacheManager:
     def fill_cuda_graph_metadata(self, bucket_size: int, real_uuids) -> None:
         """manager.py:228-253: the real sequences' page tables and the position of each one's
         newest token, then ``bucket - n`` padding rows (one padding page, last_page_len 1,
-        position 0), written into the bucket's static buffers on the device."""
+        position 0), written into the bucket's static buffers on the device.  Also fills
+        ``_cg_kv_shared[bucket]``: for consecutive rows allocated on the same prefix, the
+        prefix pages they share (the decode plan's ``kv_shared_pages``)."""
         real_uuids = list(real_uuids)
         self._flush()
         slot, staged, b, pages = self._stage_tables(real_uuids, bucket_size, positions=True)
         if pages > self._cg_kv_indices[bucket_size].numel():
             raise RuntimeError("page table larger than the bucket's kv_indices buffer")
-        # [desc | indptr | last | positions] lands in the bucket's block: the three buffers the
-        # captured step reads are views of it
+        # [desc | indptr | last | positions | shared] lands in the bucket's block: the buffers
+        # the step reads are views of it
         self._gather(slot, staged, b, pages, self._cg_kv_indices[bucket_size], dst=self._cg_meta[bucket_size],
                      slots=self._cg_slots[bucket_size])
 

@@ -223,11 +223,14 @@ class SharedPrefixDecodeLoop:
 
     Values are N(0,1)*scale from a device generator; every slot no token owns is NaN.  Lengths
     and the finished sequences come from a host generator.  With ``record=True`` every pool
-    operation is logged in ``log`` (so a test can replay it on the oracle's pool)."""
+    operation is logged in ``log`` (so a test can replay it on the oracle's pool).  With
+    ``shared_hint`` (the default) the plan is given the manager's shared-prefix hint, so the
+    prefix pages stay in L2 for their readers after the first; ``cascade`` asks the plan to read
+    the prefix once per group of sequences instead."""
 
     def __init__(self, device, *, layers=36, batch=128, hq=16, hkv=2, d=128, dtype=torch.float16,
                  prefix_tokens=2048, suffix=(64, 1024), finish=8, max_steps=64, seed=1005, scale=0.5,
-                 record=False):
+                 record=False, shared_hint=True, cascade=False):
         from .manager import AutoKVCacheManager
         from .wrappers import BatchDecodeWithPagedKVCacheWrapper
 
@@ -235,6 +238,7 @@ class SharedPrefixDecodeLoop:
         self.layers, self.batch, self.hq, self.hkv, self.d, self.dtype = layers, batch, hq, hkv, d, dtype
         self.ps = 16
         self.prefix_tokens, self.suffix, self.finish, self.scale = prefix_tokens, suffix, finish, scale
+        self.shared_hint, self.cascade = shared_hint, cascade
         self.gen = torch.Generator().manual_seed(seed + 7919)
         self.dgen = torch.Generator(device=self.device).manual_seed(seed)
         es = torch.tensor([], dtype=dtype).element_size()
@@ -318,7 +322,9 @@ class SharedPrefixDecodeLoop:
             self._note(("fill_cuda_graph_metadata", self.batch, list(self.ids)))
             self.wrapper.plan(m._cg_kv_indptr[self.batch], m._cg_kv_indices[self.batch],
                               m._cg_kv_last_page_len[self.batch], self.hq, self.hkv, self.d, self.ps,
-                              pos_encoding_mode="NONE", q_data_type=self.dtype)
+                              pos_encoding_mode="NONE", q_data_type=self.dtype,
+                              kv_shared_pages=m._cg_kv_shared[self.batch] if self.shared_hint else None,
+                              cascade=self.cascade)
 
     def layers_fn(self) -> None:
         """Every layer's append of the step's token and its decode (what the graph holds)."""

@@ -6,8 +6,9 @@ calls ``plan`` once per scheduler step with the step's page table (main.py:341-3
 hook (main.py:68), also inside captured CUDA graphs (main.py:146-148).  The classes below
 keep that call shape:
 
-* ``plan`` reads no device data and launches only one tiny kernel (zeroing the decode
-  workspace counters), so it stays cheap and never synchronises.
+* ``plan`` reads no device data on the host: the decode schedule is built on the device (two
+  small kernels, plus a fill kernel that zeroes the split counters when the batch grows), so
+  it stays cheap, never synchronises and can be captured.
 * ``run`` only enqueues kernels on the current stream and is safe to capture in a hipGraph;
   its geometry (workgroup count, kernel choice) is fixed by ``plan``'s arguments alone.
 """
@@ -51,6 +52,7 @@ def _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, ro
 
 
 _DECODE_VALU, _DECODE_DYNAMIC, _DECODE_PLANNED = 1, 2, 4  # pkv_batch_decode flags (include/pagedkv.h)
+_PLAN_CASCADE = 1  # pkv_decode_plan flag
 
 class BatchDecodeWithPagedKVCacheWrapper:
     """Paged decode attention: one query token per sequence (FlashInfer contract)."""
@@ -82,12 +84,20 @@ class BatchDecodeWithPagedKVCacheWrapper:
              pos_encoding_mode: str = "NONE", window_left: int = -1, logits_soft_cap=None,
              q_data_type="float16", kv_data_type=None, data_type=None, sm_scale=None,
              rope_scale=None, rope_theta=None, non_blocking: bool = True,
-             num_ctas: int | None = None, deterministic: bool = True, **_unused) -> None:
+             num_ctas: int | None = None, deterministic: bool = True,
+             kv_shared_pages: torch.Tensor | None = None, cascade: bool = False, **_unused) -> None:
         """Extensions: ``num_ctas`` fixes the number of workgroups that share the batch's
         pages (by default one per compute unit for the matrix-core kernel);
         ``deterministic=False`` lets the waves of a workgroup take pages on demand, which is
         a little faster but makes the last bits of the result vary from call to call (with
-        the default the result is bitwise reproducible, as FlashInfer's is)."""
+        the default the result is bitwise reproducible, as FlashInfer's is);
+        ``kv_shared_pages`` (int32 [batch] on the device, as
+        ``AutoKVCacheManager.fill_cuda_graph_metadata`` leaves it in ``_cg_kv_shared``) says,
+        for each sequence b >= 1, how many of its leading pages are the same pages as sequence
+        b - 1's (the caller guarantees the pages agree, as it does for the rest of the page
+        table): a prefix that runs of sequences share is then kept in L2 for its readers after
+        the first, and with ``cascade=True`` it is read once per group of up to 32 sequences
+        instead (include/pagedkv.h, pkv_decode_plan)."""
         _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, rope_theta)
         self._indptr = _i32(indptr, "indptr")
         self._indices = _i32(indices, "indices")
@@ -128,11 +138,18 @@ class BatchDecodeWithPagedKVCacheWrapper:
                                                   stream_ptr(dev)), "decode plan")
             self._counters_ready = self._batch
         self._flags = 0 if deterministic else _DECODE_DYNAMIC
+        shared = 0
+        if kv_shared_pages is not None:
+            self._shared = _i32(kv_shared_pages, "kv_shared_pages")
+            if self._shared.numel() < self._batch:
+                raise ValueError("kv_shared_pages must have one entry per sequence")
+            shared = self._shared.data_ptr()
         if self._mfma:
             # the matrix-core kernel's schedule, built on the device from this page table
             check(lib().pkv_decode_plan(self._indptr.data_ptr(), self._indices.data_ptr(),
-                                        self._indices.numel(), self._last.data_ptr(), self._batch,
+                                        self._indices.numel(), self._last.data_ptr(), shared, self._batch,
                                         self._hq, self._hkv, self._d, self._ps, self._ctas,
+                                        _PLAN_CASCADE if cascade else 0,
                                         self._workspace.data_ptr(),
                                         self._workspace.numel() * self._workspace.element_size(),
                                         stream_ptr(dev)), "decode plan")

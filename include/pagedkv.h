@@ -102,10 +102,12 @@ int pkv_append_paged_kv_cache_rope(const void* q, int64_t q_stride_n, int64_t q_
                                    int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                    int32_t dtype, int32_t* err_count, void* stream);
 
-/* Workspace bytes pkv_decode_plan and pkv_batch_decode need for this geometry (num_indices =
+/* Smallest workspace pkv_decode_plan and pkv_batch_decode need for this geometry (num_indices =
  * length of the kv_indices buffer): the host half of BatchDecodeWithPagedKVCacheWrapper.plan
  * (ecahlang/main.py:341-347, :444-455).  The reference hands the wrapper a 128 MiB buffer
- * (ecahlang/main.py:203). */
+ * (ecahlang/main.py:203).  A larger workspace also holds the partial results of shared-prefix
+ * chunks (see pkv_decode_plan); the layout depends on the size, so pass plan and decode the
+ * same workspace_bytes. */
 int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
                                    int32_t num_ctas, int64_t num_indices);
 
@@ -115,19 +117,32 @@ int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t 
 int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream);
 
 /* The device half of BatchDecodeWithPagedKVCacheWrapper.plan (ecahlang/main.py:341-347,
- * :444-455, :538-548): one kernel reads the page table (kv_indptr, kv_indices, kv_last_page_len)
- * and writes the matrix-core kernel's schedule into the workspace: the batch's pages cut into
- * ranges (about one per workgroup, at most 512 pages each; a range that holds a sequence start
- * gets fewer pages, since its waves combine their states there), each with its sequence
- * segments and a copy of its page ids.  FlashInfer's plan computes its schedule on the host after copying
- * kv_indptr back; this one never synchronises and can be captured.  Every decode launch on the
- * same workspace with PKV_DECODE_PLANNED reads it, so the page table it was built from must not
- * change before those launches (re-plan after rebuilding it, as the reference does before each
- * step). */
+ * :444-455, :538-548): two kernels read the page table (kv_indptr, kv_indices,
+ * kv_last_page_len) and write the matrix-core kernel's schedule into the workspace: the batch's
+ * pages cut into ranges (about one per workgroup, at most 512 pages each; a range that holds a
+ * sequence start gets fewer pages, since its waves combine their states there), each with its
+ * sequence segments and a copy of its page ids.  FlashInfer's plan computes its schedule on the
+ * host after copying kv_indptr back; this one never synchronises and can be captured.  Every
+ * decode launch on the same workspace with PKV_DECODE_PLANNED reads it, so the page table it
+ * was built from must not change before those launches (re-plan after rebuilding it, as the
+ * reference does before each step).
+ *
+ * kv_shared_pages (an extension; may be NULL) describes shared prefixes: entry b >= 1 says
+ * that the first kv_shared_pages[b] pages of sequence b are the same page ids as the first ones
+ * of sequence b - 1 (entry 0 is ignored; the caller guarantees it, as it guarantees the rest of
+ * the page table).  The common prefix of a run of consecutive sequences that share at least 16
+ * pages is then copied with the cached load policy, so every reader after the first finds it in
+ * L2 (other pages stream past the caches).  With PKV_PLAN_CASCADE in plan_flags, the common
+ * prefix is instead read once per group of up to 32 sequences (one workgroup attends the whole
+ * group to it, per KV head, and the parts are merged like split sequences); the results are
+ * those of the plain schedule up to the order of the fp32 summation.  AutoKVCacheManager fills
+ * kv_shared_pages for sequences allocated on a prefix. */
+#define PKV_PLAN_CASCADE 1
 int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
-                    const int32_t* kv_last_page_len, int32_t batch, int32_t num_qo_heads,
-                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t num_ctas,
-                    void* workspace, int64_t workspace_bytes, void* stream);
+                    const int32_t* kv_last_page_len, const int32_t* kv_shared_pages, int32_t batch,
+                    int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                    int32_t num_ctas, int32_t plan_flags, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /* 1 when pkv_batch_decode can run the matrix-core kernel for this shape (fp16/bf16, head_dim
  * 64 or 128, group <= 16, and num_kv_heads at most 8 head blocks of up to 256 / head_dim heads;

@@ -52,9 +52,13 @@ def _check_layer(loop, layer, rows, idx, ptr, last):
         np.testing.assert_allclose(got, ref, atol=2e-3, rtol=1e-2, err_msg=f"layer {layer} row {r}")
 
 
-def test_small_loop_matches_oracle_every_step():
+@pytest.mark.parametrize("hint,cascade", [(True, False), (False, False), (True, True)])
+def test_small_loop_matches_oracle_every_step(hint, cascade):
+    """With the manager's shared-prefix hint (the prefix's pages kept in L2), without it, and
+    with the cascade (the prefix read once per group)."""
     loop = workloads.SharedPrefixDecodeLoop(DEV, layers=3, batch=16, prefix_tokens=256, suffix=(1, 200),
-                                            finish=4, max_steps=12, seed=7, record=True)
+                                            finish=4, max_steps=12, seed=7, record=True,
+                                            shared_hint=hint, cascade=cascade)
     ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
     done = 0
     for step in range(8):

@@ -25,6 +25,7 @@ def _mirror(ref: RefKVCacheManager) -> AutoKVCacheManager:
     m._npages = {b: len(p) for b, p in ref.batch_to_blocks.items()}
     m._n_padding = len(ref.padding_pages)
     m._rows = ref.seq_lens + 1
+    m._shared = dict(ref.shared)
     m._staging = _HostStaging()
     return m
 
@@ -39,7 +40,12 @@ def _random_pool(seed):
         n = rng.choice([0, 1, 1, 2, 15, 16, 17, 40])
         try:
             if sid not in ref.batch_to_blocks:
-                ref.allocate(sid, n)
+                pre = [p for p in ref.batch_to_blocks if ref.seq_len(p) >= 16]
+                if pre and rng.random() < 0.5:  # on a live sequence's full pages
+                    p = rng.choice(pre)
+                    ref.allocate(sid, ref.seq_len(p) // 16 * 16 + n, prefix=p)
+                else:
+                    ref.allocate(sid, n)
             elif rng.random() < 0.15:
                 ref.free(sid)
             else:
@@ -54,8 +60,10 @@ def test_staged_tables_match_oracle(seed):
     rng, ref = _random_pool(seed)
     m = _mirror(ref)
     live = list(ref.batch_to_blocks)
-    for _ in range(20):
+    for it in range(20):
         ids = rng.sample(live, rng.randint(0, len(live)))
+        if it % 2:  # rows on one prefix next to each other, as a serving batch groups them
+            ids.sort(key=lambda i: str(ref.shared.get(i, ("",))[0]))
         # get_append_metadata: [desc | indptr | last_page_len]
         _, out, b, pages = m._stage_tables(ids)
         idx, ptr, last = ref.get_append_metadata(ids)
@@ -70,10 +78,23 @@ def test_staged_tables_match_oracle(seed):
             continue
         _, out, b, pages = m._stage_tables(ids, bucket, positions=True)
         idx, ptr, last, pos = ref.fill_cuda_graph_metadata(bucket, ids)
-        assert b == bucket and pages == len(idx) and out.size == 7 * b + 1
+        assert b == bucket and pages == len(idx) and out.size == 8 * b + 1
         assert out[4 * b: 5 * b + 1].tolist() == ptr
         assert out[5 * b + 1: 6 * b + 1].tolist() == last
-        assert out[6 * b + 1:].tolist() == pos
+        assert out[6 * b + 1: 7 * b + 1].tolist() == pos
+        # the decode plan's hint: never more pages than the two rows' page lists share, and
+        # every page two rows allocated on one prefix share
+        shared = out[7 * b + 1:].tolist()
+        assert shared[0] == 0 and shared[len(ids):] == [0] * (bucket - len(ids))
+        for k in range(1, len(ids)):
+            a, c = ref.batch_to_blocks[ids[k - 1]], ref.batch_to_blocks[ids[k]]
+            h = shared[k]
+            assert a[:h] == c[:h], (ids[k - 1], ids[k], h)
+            pa, pc = ref.shared.get(ids[k - 1]), ref.shared.get(ids[k])
+            if pa and pc and pa[0] == pc[0]:
+                assert h == min(pa[1], pc[1])
+            else:
+                assert h == 0
         desc = out[: 4 * b].reshape(b, 4).tolist()
         real = [[ref.batch_to_seq_len[i], 0, len(ref.batch_to_blocks[i]), 0] for i in ids]
         pad = [[m._rows - 1, i, 1, 0] for i in range(bucket - len(ids))]
