@@ -43,6 +43,7 @@ struct DecodeParams {
   const int32_t* sched_hdr;    // ... and its global header
   const int32_t* sched_head;   // ... and the dense heads of its ranges
   const int32_t* sched_pref;   // ... and its prefix item records
+  int32_t cascade;             // the schedule was planned with prefix items
   int32_t r_cap;               // ranges the workspace holds
 };
 

@@ -16,6 +16,7 @@
 // chunks when the workspace has room (each part_ml slot is whole 128-byte lines).  The layout
 // depends on the workspace size, so plan and run are given the same size.
 #include <mutex>
+#include <unordered_map>
 #include "attn_common.h"
 #include "decode_sched.h"
 #include "../../include/pagedkv.h"
@@ -70,6 +71,11 @@ inline WsLayout ws_layout(int batch, int hq, int d, int ctas, int64_t num_indice
   return L;
 }
 
+// Which workspaces hold a cascade schedule (the decode launches the kernel variant that reads
+// prefix items only for those): recorded by pkv_decode_plan, read by pkv_batch_decode.
+std::mutex g_plan_mu;
+std::unordered_map<const void*, bool> g_plan_cascade;
+
 __global__ void zero_i32_kernel(int32_t* p, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
@@ -116,9 +122,15 @@ extern "C" int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indic
   if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
   char* ws = (char*)workspace;
   const int group = decode_mfma_group(head_dim, num_qo_heads / num_kv_heads, num_kv_heads);
+  const bool cascade = (plan_flags & PKV_PLAN_CASCADE) && kv_shared_pages && group >= 2;
+  {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    if (cascade) g_plan_cascade[workspace] = true;
+    else g_plan_cascade.erase(workspace);
+  }
   return decode_plan_launch(kv_indptr, kv_indices, num_indices, kv_last_page_len, kv_shared_pages,
                             batch, num_ctas, page_size, seg_cost_pages(num_kv_heads, head_dim, page_size),
-                            group, num_kv_heads, (plan_flags & PKV_PLAN_CASCADE) ? 1 : 0, (int)L.rcap,
+                            group, num_kv_heads, cascade ? 1 : 0, (int)L.rcap,
                             (int)L.slots, (int32_t*)(ws + L.ghdr),
                             (int32_t*)(ws + L.recs), (int32_t*)(ws + L.heads), (int32_t*)(ws + L.precs),
                             (int32_t*)(ws + L.bf), (int32_t*)(ws + L.starts), (int32_t*)(ws + L.nzb),
@@ -168,6 +180,11 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   P.sched = (const int32_t*)(ws + L.recs);
   P.sched_head = (const int32_t*)(ws + L.heads);
   P.sched_pref = (const int32_t*)(ws + L.precs);
+  {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    const auto it = g_plan_cascade.find(workspace);
+    P.cascade = it != g_plan_cascade.end() && it->second;
+  }
   P.slot_cap = (int32_t)L.slots;
   P.r_cap = (int32_t)L.rcap;
   P.num_ctas = num_ctas;

@@ -135,7 +135,9 @@ struct Shape {
   static constexpr int LDS = W * 2 * TILE + kQArea;  // dynamic LDS
 };
 
-template <typename T, int D, int HB>
+// CASC: the schedule may hold prefix items (a cascade plan).  Without it the prefix-item code is
+// not compiled in, which keeps the range loop's registers free of its pressure.
+template <typename T, int D, int HB, bool CASC>
 __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   using S = Shape<HB, D>;
   constexpr int RB = S::RB, CPR = S::CPR, RPI = S::RPI, NI = S::NI, TILE = S::TILE;
@@ -467,7 +469,9 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     nseg = nseg < 0 ? 0 : (nseg > len ? len : nseg);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // round 1 complete (compiler-visible vmcnt(0))
     if (w >= rmax) break;
-    if (__builtin_amdgcn_readlane(hv, kHdrPrefix)) prefix_item(w);
+    if constexpr (CASC) {
+      if (__builtin_amdgcn_readlane(hv, kHdrPrefix)) prefix_item(w);
+    }
     if (nseg == 0) continue;
     // segment s < kHeadSegs from the round-1 registers
     auto seg_reg = [&](int s) __attribute__((always_inline)) -> int4 {
@@ -767,7 +771,10 @@ int head_block(int d, int g, int hkv) {
 template <typename T, int D, int HB>
 int launch(const DecodeParams& P, hipStream_t s) {
   constexpr int lds = Shape<HB, D>::LDS;
-  hipLaunchKernelGGL((decode_mfma_kernel<T, D, HB>), dim3(P.num_ctas), dim3(NT), lds, s, P);
+  if (P.cascade)
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, HB, true>), dim3(P.num_ctas), dim3(NT), lds, s, P);
+  else
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, HB, false>), dim3(P.num_ctas), dim3(NT), lds, s, P);
   return (int)hipGetLastError();
 }
 
