@@ -16,6 +16,11 @@
 //                       prefix's full pages; no counterpart in the reference)
 //   pkv_pool_gather  <- get_append_metadata / fill_cuda_graph_metadata (the page walk that
 //                       builds kv_indices, manager.py:124-133, 231-246)
+//   pkv_pool_step    <- one decode step of a fixed batch, all on the device: append_tokens(b, n)
+//                       for every row (manager.py:187-205) then fill_cuda_graph_metadata for
+//                       the bucket (manager.py:228-253), with the per-slot page counts and
+//                       last-page lengths kept on the device, so the step can be replayed from
+//                       a graph with no host work in between
 #include "common.h"
 #include "../../include/pagedkv.h"
 
@@ -96,6 +101,107 @@ __global__ void pool_gather_kernel(const int32_t* table, int64_t stride, int32_t
   }
 }
 
+// One workgroup: appends n tokens to every real row of the bucket, in row order (the order of
+// the reference's append_tokens loop), popping the pages that fill from the top of the stack
+// exactly as append_tokens would (row i's pops come after rows 0 .. i-1's), then writes the
+// bucket's metadata: kv_indptr, kv_last_page_len, each row's newest-token position, and the
+// gather descriptor pool_gather_kernel reads.  Padding rows (rows[i] < 0) take one padding
+// page each, in order (last_page_len 1, position 0).  A row whose pops the stack (or its table row)
+// cannot hold is left unchanged, as are all rows after it, and *err is bumped: the host checks
+// the pool before it enqueues a step, so this is only a guard.
+constexpr int kStepThreads = 1024;
+__global__ __launch_bounds__(kStepThreads) void pool_step_kernel(
+    int32_t* stack, int32_t* n_free, int32_t* table, int64_t stride, int32_t rows_total,
+    const int32_t* rows, int32_t batch, int32_t n_tokens, int32_t bs, int32_t* npages, int32_t* plen,
+    int32_t padding_row, int32_t* desc, int32_t* indptr, int32_t* last, int32_t* positions, int32_t* err) {
+  __shared__ int s_wsum[kStepThreads / 64];
+  __shared__ int s_free, s_fail, s_taken;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tid == 0) {
+    s_free = *n_free;
+    s_fail = batch;
+    s_taken = 0;
+  }
+  __syncthreads();
+  const int nf = s_free;
+  auto scan = [&](int v, int& carry) -> int {  // block-wide exclusive scan (all threads call it)
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      x += lane >= off ? y : 0;
+    }
+    if (lane == 63) s_wsum[wv] = x;
+    __syncthreads();
+    int o = 0, blk = 0;
+#pragma unroll
+    for (int k = 0; k < kStepThreads / 64; ++k) {
+      o += k < wv ? s_wsum[k] : 0;
+      blk += s_wsum[k];
+    }
+    const int ex = carry + o + x - v;
+    carry += blk;
+    __syncthreads();
+    return ex;
+  };
+  auto real_row = [&](int i) -> int {
+    const int row = i < batch ? rows[i] : -1;
+    return row >= 0 && row < rows_total ? row : -1;
+  };
+  // ---- pops: row i needs (plen + n) / bs pages, taken from the top after rows 0 .. i-1's
+  int before = 0;
+  for (int base = 0; base < batch; base += kStepThreads) {
+    const int i = base + tid;
+    const int row = real_row(i);
+    int need = 0, np = 0, pl = 0;
+    if (row >= 0) {
+      np = npages[row];
+      pl = plen[row];
+      need = (pl + n_tokens) / bs;
+    }
+    const int off = scan(need, before);
+    if (row >= 0 && (off + need > nf || (int64_t)np + need > stride)) atomicMin(&s_fail, i);
+    __syncthreads();
+    if (row >= 0 && i < s_fail) {
+      int32_t* trow = table + (int64_t)row * stride + np;
+      for (int k = 0; k < need; ++k) trow[k] = stack[nf - 1 - off - k];
+      npages[row] = np + need;
+      plen[row] = (pl + n_tokens) % bs;
+      if (need) atomicAdd(&s_taken, need);
+    }
+    __syncthreads();
+    if (s_fail < batch) break;  // (uniform)
+  }
+  if (tid == 0) {
+    *n_free = nf - s_taken;
+    if (s_fail < batch && err) atomicAdd(err, 1);
+  }
+  // ---- the bucket's metadata, from the new counts (padding entry j takes padding page j)
+  int carry = 0, pads = 0;
+  for (int base = 0; base < batch; base += kStepThreads) {
+    const int i = base + tid;
+    const int row = real_row(i);
+    int np = 1, pl = 1, pos = 0;
+    if (row >= 0) {
+      np = npages[row];
+      pl = plen[row];
+      pos = (np - 1) * bs + pl - 1;
+    }
+    const int start = scan(i < batch ? np : 0, carry);
+    const int pad = scan(i < batch && row < 0 ? 1 : 0, pads);
+    if (i < batch) {
+      indptr[i] = start;
+      last[i] = pl;
+      positions[i] = pos;
+      desc[4 * i] = row >= 0 ? row : padding_row;
+      desc[4 * i + 1] = row >= 0 ? 0 : pad;
+      desc[4 * i + 2] = np;
+      desc[4 * i + 3] = 0;
+    }
+  }
+  if (tid == 0) indptr[batch] = carry;
+}
+
 }  // namespace
 
 extern "C" int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
@@ -122,6 +228,31 @@ extern "C" int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t row
   blocks = blocks < 1024 ? (blocks > 0 ? blocks : 1) : 1024;
   hipLaunchKernelGGL(pool_gather_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream,
                      table, stride, rows, desc, indptr, batch, indices, num_indices, positions, page_size,
+                     slots, err);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_pool_step(int32_t* stack, int32_t* n_free, int32_t* table, int64_t stride,
+                             int32_t rows_total, const int32_t* rows, int32_t batch, int32_t n_tokens,
+                             int32_t page_size, int32_t* npages, int32_t* last_len, int32_t padding_row,
+                             int32_t* desc, int32_t* kv_indptr, int32_t* kv_last_page_len,
+                             int32_t* positions, int32_t* kv_indices, int64_t num_indices,
+                             int64_t max_total, int32_t* slots, int32_t* err, void* stream) {
+  if (batch <= 0 || n_tokens < 0 || page_size <= 0 || stride <= 0 || rows_total <= 0 || num_indices < 0 ||
+      max_total < 0 || padding_row < 0 || padding_row >= rows_total)
+    return kBadArg;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(pool_step_kernel, dim3(1), dim3(kStepThreads), 0, s, stack, n_free, table, stride,
+                     rows_total, rows, batch, n_tokens, page_size, npages, last_len, padding_row, desc,
+                     kv_indptr, kv_last_page_len, positions, err);
+  // kv_indices and the append slots, as fill_cuda_graph_metadata's gather
+  int64_t n = max_total < num_indices ? max_total : num_indices;
+  if (n < batch) n = batch;
+  const int threads = 256;
+  int64_t blocks = (n + threads - 1) / threads;
+  blocks = blocks < 1024 ? (blocks > 0 ? blocks : 1) : 1024;
+  hipLaunchKernelGGL(pool_gather_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, table, stride,
+                     rows_total, desc, kv_indptr, batch, kv_indices, num_indices, positions, page_size,
                      slots, err);
   return (int)hipGetLastError();
 }

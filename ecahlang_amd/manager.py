@@ -63,7 +63,8 @@ class _Staging:
     its last copy has completed (so a queued copy never sees its source change); ``send`` queues
     the copy and records the buffer's event.  Arrays beyond the ring's capacity, and copies made
     while the stream is being captured, go through a fresh pinned buffer instead, which the
-    caching host allocator keeps until its copy has run."""
+    caching host allocator keeps until its copy has run; a copy recorded into a graph reads its
+    buffer at every replay, so those buffers are kept for the life of the staging ring."""
 
     def __init__(self, device: torch.device, slots: int = 8, cap: int = 1 << 15):
         self.device, self.cap = device, cap
@@ -72,6 +73,7 @@ class _Staging:
         self.events = [torch.cuda.Event() for _ in range(slots)]
         self.used = [False] * slots
         self.i = 0
+        self.captured: list = []  # pinned sources of copies recorded into graphs
 
     def host(self, n: int) -> tuple:
         """(slot, int32 array of n to fill); slot -1 means the array is not a ring buffer."""
@@ -88,6 +90,8 @@ class _Staging:
         ``dst`` is None."""
         n = len(arr)
         src = self.bufs[slot][:n] if slot >= 0 else torch.from_numpy(arr).pin_memory()
+        if slot < 0 and torch.cuda.is_current_stream_capturing():
+            self.captured.append(src)
         if dst is None:
             dst = torch.empty(n, dtype=torch.int32, device=self.device)
         dst[:n].copy_(src, non_blocking=True)
@@ -207,6 +211,12 @@ class AutoKVCacheManager:
         self._stride = max(1, min(max(self.max_blocks, 1), max_pages_per_seq))
         self._table = torch.full((self._rows, self._stride), -1, dtype=torch.int32, device=self.device)
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        # device-resident decode steps (begin_device_steps): each slot's page count and
+        # last-page length, and the free-stack size, as the device advances them
+        self._dev_npages = torch.zeros(self._rows, dtype=torch.int32, device=self.device)
+        self._dev_plen = torch.zeros(self._rows, dtype=torch.int32, device=self.device)
+        self._dev_nfree = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._dev = None  # the batch handed to the device, or None
         self._staging = _Staging(self.device)
         self._ops: list = []
         self._n_padding = 0
@@ -234,6 +244,8 @@ class AutoKVCacheManager:
         # bucket -> for each row, the leading pages it shares with the row before it (the
         # decode plan's kv_shared_pages)
         self._cg_kv_shared: dict = {}
+        self._cg_rows: dict = {}   # bucket -> table row of each batch entry (-1: padding), device steps
+        self._cg_desc: dict = {}   # bucket -> gather descriptor scratch of the device step
         # The pool's initial state (free stack, page table, cache) is written on the current
         # stream; a caller may go on to drive the pool from another stream, so it is complete
         # before the constructor returns.
@@ -242,6 +254,7 @@ class AutoKVCacheManager:
     # ------------------------------------------------------------------ device pool plumbing
 
     def _ensure_stride(self, need: int) -> None:
+        self._end_dev()
         if need <= self._stride:
             return
         new = max(need, 2 * self._stride)
@@ -251,6 +264,7 @@ class AutoKVCacheManager:
 
     def _flush(self) -> None:
         """Apply the queued pops and pushes (one launch, in order, on the current stream)."""
+        self._end_dev()
         if not self._ops:
             return
         flat = [x for op in self._ops for x in op]
@@ -266,6 +280,7 @@ class AutoKVCacheManager:
         array: [desc (4 per row) | kv_indptr (rows + 1) | kv_last_page_len (rows)] plus
         [positions (rows) | shared (rows)] (each row's newest token, and how many leading pages
         it shares with the row before it) when asked.  Returns (slot, array, rows, pages)."""
+        self._end_dev()
         r = len(ids)
         b = max(bucket, r)
         if b - r > self._n_padding:
@@ -351,14 +366,33 @@ class AutoKVCacheManager:
 
     # ------------------------------------------------------------------ page pool (A3-A5)
 
+    def _counts(self, batch_id) -> tuple:
+        """(pages, last-page length) of a sequence, also while the device runs its steps."""
+        d = self._dev
+        if d is not None and batch_id in d["at"]:
+            i = d["at"][batch_id]
+            return self._advanced(d["npages0"][i], d["plen0"][i], d["k"] * d["n"])
+        return self._npages[batch_id], self.batch_to_page_lengths[batch_id]
+
+    def _advanced(self, npages: int, last: int, tokens: int) -> tuple:
+        """(pages, last-page length) after appending `tokens` tokens one step at a time, each
+        step as append_tokens does it: t = last + n, pop t // block_size, keep t % block_size.
+        With last <= block_size that is (last + tokens) // block_size pops in all (the last
+        page may start full: allocate's last_page_len of block_size)."""
+        if tokens == 0:
+            return npages, last
+        t = last + tokens
+        return npages + t // self.block_size, t % self.block_size
+
     def _seq_len(self, batch_id) -> int:
-        n = self._npages[batch_id]
-        return (n - 1) * self.block_size + self.batch_to_page_lengths[batch_id] if n else 0
+        n, last = self._counts(batch_id)
+        return (n - 1) * self.block_size + last if n else 0
 
     def allocate(self, batch_id, total_tokens: int, *, prefix=None) -> _Pages:
         """manager.py:99-112: pop ceil(T / block_size) pages, take a sequence slot.  With
         ``prefix`` (an extension), the full pages of that live sequence come first and only
         the rest are popped."""
+        self._end_dev()
         shared = 0
         if prefix is not None:
             if prefix not in self._npages:
@@ -395,6 +429,7 @@ class AutoKVCacheManager:
     def free(self, batch_id) -> None:
         """manager.py:114-120: push the pages back in page order, release the slot (a
         sequence's shared prefix pages stay with the prefix)."""
+        self._end_dev()
         if self._refs.get(batch_id):
             raise RuntimeError(f"{batch_id} is the shared prefix of {self._refs[batch_id]} live sequences")
         n = self._npages.pop(batch_id, 0)
@@ -412,6 +447,7 @@ class AutoKVCacheManager:
     def append_tokens(self, batch_id, num_new_tokens: int) -> None:
         """manager.py:187-205: a page is popped as soon as the last one fills (an empty
         trailing page with last_page_len 0 is kept, as the reference does)."""
+        self._end_dev()
         if batch_id not in self._npages:
             raise ValueError(f"{batch_id} not allocated")
         current_len = self.batch_to_page_lengths.get(batch_id, 0)
@@ -480,6 +516,7 @@ class AutoKVCacheManager:
         buffers the captured step reads.  ``max_indices`` (an extension) sizes the static
         ``kv_indices`` buffers; the reference's ``max_blocks`` is too small once sequences
         share prefix pages (a shared page appears in every table that holds it)."""
+        self._end_dev()
         max_bucket = max(bucket_sizes)
         if self._n_free < max_bucket:
             raise RuntimeError(f"Not enough free blocks for {max_bucket} padding pages")
@@ -501,6 +538,8 @@ class AutoKVCacheManager:
             self._cg_batch_indices[bs] = torch.arange(bs, dtype=torch.int32, device=dev)
             self._cg_positions[bs] = meta[6 * bs + 1: 7 * bs + 1]
             self._cg_kv_shared[bs] = meta[7 * bs + 1: 8 * bs + 1]
+            self._cg_rows[bs] = torch.full((bs,), -1, dtype=torch.int32, device=dev)
+            self._cg_desc[bs] = torch.zeros(4 * bs, dtype=torch.int32, device=dev)
             self._cg_slots[bs] = torch.full((bs,), -1, dtype=torch.int32, device=dev)
             self._cg_append_indptr[bs] = torch.arange(bs + 1, dtype=torch.int32, device=dev)
             self._cg_temperature[bs] = torch.ones(bs, 1, dtype=torch.float32, device=dev)
@@ -530,6 +569,108 @@ class AutoKVCacheManager:
         layer's append reads one slot per token."""
         append_paged_kv_cache_slots(key, value, self._cg_slots[bucket_size], self.kv_cache[layer_idx],
                                     kv_layout=self.layout)
+
+    # ------------------------------------------------------------------ device-resident decode steps
+
+    def begin_device_steps(self, bucket_size: int, real_uuids, steps: int, num_new_tokens: int = 1) -> None:
+        """Extension: hand the next ``steps`` decode steps of this batch to the device.
+
+        Each step is the serving loop's ``append_tokens(b, num_new_tokens)`` for every sequence
+        of ``real_uuids`` (in that order) followed by ``fill_cuda_graph_metadata(bucket_size,
+        real_uuids)`` (ecahlang/main.py:328-347), done by ``device_step`` on the device with no
+        host work, so it can be captured in a graph together with the plan and the model and
+        replayed.  Per replay the host calls ``advance_device_step`` (O(1): it advances the free
+        count by the pages the step pops, which it knows in advance).  Sets up the bucket's
+        buffers for the current state (as ``fill_cuda_graph_metadata`` would) and widens the
+        page table for ``steps`` steps, before any capture: the table must not move while a
+        graph holds its address.  Any other method of the manager first brings the host
+        counts up to date (``end_device_steps``)."""
+        self._end_dev()
+        ids = list(real_uuids)
+        bs = self.block_size
+        if steps < 0 or num_new_tokens < 0:
+            raise ValueError("steps and num_new_tokens must be non-negative")
+        grow = -(-(steps * num_new_tokens) // bs) + 1  # pages a sequence can gain
+        if ids:
+            self._ensure_stride(max(self._npages[i] for i in ids) + grow)
+        cap = self._cg_kv_indices[bucket_size].numel()
+        if sum(self._npages[i] for i in ids) + len(ids) * grow + bucket_size - len(ids) > cap:
+            raise RuntimeError("page table of the device steps larger than the bucket's kv_indices buffer")
+        self.fill_cuda_graph_metadata(bucket_size, ids)
+        rows = [self.batch_to_seq_len[i] for i in ids]
+        npages = [self._npages[i] for i in ids]
+        plen = [self.batch_to_page_lengths[i] for i in ids]
+        staged = self._staging.copy(rows + [-1] * (bucket_size - len(ids)) + npages + plen)
+        self._cg_rows[bucket_size].copy_(staged[:bucket_size])
+        if ids:
+            idx = staged[:len(ids)].long()
+            self._dev_npages.index_copy_(0, idx, staged[bucket_size: bucket_size + len(ids)])
+            self._dev_plen.index_copy_(0, idx, staged[bucket_size + len(ids):])
+        self._dev_nfree.fill_(self._n_free)
+        # one token a step: a row with last-page length p pops at the steps k with p + k a
+        # multiple of bs, and a row whose last page starts full (p == bs) also pops at step 1
+        hist = np.zeros(bs, dtype=np.int64)
+        for p in plen:
+            hist[p % bs] += 1
+        self._dev = {"bucket": bucket_size, "ids": ids, "at": {i: j for j, i in enumerate(ids)},
+                     "npages0": npages, "plen0": plen, "hist": hist, "full": sum(p == bs for p in plen),
+                     "n": num_new_tokens, "k": 0, "max": steps}
+
+    def device_step(self, bucket_size: int) -> None:
+        """Enqueue one device step of the batch given to ``begin_device_steps`` (no host work;
+        safe to capture): ``pkv_pool_step`` over the bucket's static buffers."""
+        d = self._dev
+        if d is None or d["bucket"] != bucket_size:
+            raise RuntimeError("begin_device_steps must be called for this bucket first")
+        idx = self._cg_kv_indices[bucket_size]
+        check(lib().pkv_pool_step(self._stack.data_ptr(), self._dev_nfree.data_ptr(), self._table.data_ptr(),
+                                  self._stride, self._rows, self._cg_rows[bucket_size].data_ptr(), bucket_size,
+                                  d["n"], self.block_size, self._dev_npages.data_ptr(), self._dev_plen.data_ptr(),
+                                  self._rows - 1, self._cg_desc[bucket_size].data_ptr(),
+                                  self._cg_kv_indptr[bucket_size].data_ptr(),
+                                  self._cg_kv_last_page_len[bucket_size].data_ptr(),
+                                  self._cg_positions[bucket_size].data_ptr(), idx.data_ptr(), idx.numel(),
+                                  idx.numel(), self._cg_slots[bucket_size].data_ptr(), self._err.data_ptr(),
+                                  stream_ptr(self.device)), "device decode step")
+
+    def advance_device_step(self, bucket_size: int) -> None:
+        """The host side of one replay of ``device_step`` (call it once per replay, before it).
+        When the step would need more free pages than the pool has, the host counts are
+        brought up to date and the reference's per-sequence path runs instead, which raises
+        ``RuntimeError("Not enough free blocks to append tokens")`` at the same sequence as the
+        reference (the sequences before it are appended); the graph must then not be
+        replayed."""
+        d = self._dev
+        if d is None or d["bucket"] != bucket_size:
+            raise RuntimeError("begin_device_steps must be called for this bucket first")
+        k = d["k"] + 1
+        if k > d["max"]:
+            raise RuntimeError(f"begin_device_steps was given {d['max']} steps")
+        bs, n = self.block_size, d["n"]
+        if n == 1:
+            pops = int(d["hist"][(-k) % bs]) + (d["full"] if k == 1 else 0)
+        else:
+            pops = sum(self._advanced(0, p, k * n)[0] - self._advanced(0, p, (k - 1) * n)[0] for p in d["plen0"])
+        if pops > self._n_free:
+            ids = d["ids"]
+            self._end_dev()
+            for i in ids:  # raises at the first sequence the pool cannot serve
+                self.append_tokens(i, n)
+            raise RuntimeError("Not enough free blocks to append tokens")
+        self._n_free -= pops
+        d["k"] = k
+
+    def end_device_steps(self) -> None:
+        """Bring the host counts of the device's batch up to date (the steps it has run)."""
+        self._end_dev()
+
+    def _end_dev(self) -> None:
+        d = self._dev
+        if d is None:
+            return
+        self._dev = None
+        for i, n0, p0 in zip(d["ids"], d["npages0"], d["plen0"]):
+            self._npages[i], self.batch_to_page_lengths[i] = self._advanced(n0, p0, d["k"] * d["n"])
 
     # ------------------------------------------------------------------ sampling buffers (outside the path)
     # main.py reads sampling_{temperature,top_k,top_p}_gpu and the bucket's _cg_* copies of

@@ -226,11 +226,14 @@ class SharedPrefixDecodeLoop:
     operation is logged in ``log`` (so a test can replay it on the oracle's pool).  With
     ``shared_hint`` (the default) the plan is given the manager's shared-prefix hint, so the
     prefix pages stay in L2 for their readers after the first; ``cascade`` asks the plan to read
-    the prefix once per group of sequences instead."""
+    the prefix once per group of sequences instead.  With ``device_steps`` the step's
+    append_tokens and metadata run on the device (AutoKVCacheManager.begin_device_steps) and the
+    graph holds the whole step: page-table step, plan, and every layer's append + decode; the
+    host's per-step work is ``advance_device_step``."""
 
     def __init__(self, device, *, layers=36, batch=128, hq=16, hkv=2, d=128, dtype=torch.float16,
                  prefix_tokens=2048, suffix=(64, 1024), finish=8, max_steps=64, seed=1005, scale=0.5,
-                 record=False, shared_hint=True, cascade=False):
+                 record=False, shared_hint=True, cascade=False, device_steps=False):
         from .manager import AutoKVCacheManager
         from .wrappers import BatchDecodeWithPagedKVCacheWrapper
 
@@ -239,15 +242,18 @@ class SharedPrefixDecodeLoop:
         self.ps = 16
         self.prefix_tokens, self.suffix, self.finish, self.scale = prefix_tokens, suffix, finish, scale
         self.shared_hint, self.cascade = shared_hint, cascade
+        self.device_steps, self.max_steps = device_steps, max_steps
         self.gen = torch.Generator().manual_seed(seed + 7919)
         self.dgen = torch.Generator(device=self.device).manual_seed(seed)
         es = torch.tensor([], dtype=dtype).element_size()
         self.page_bytes = 2 * self.ps * hkv * d * es  # one page of one layer
         own_max = -(-(suffix[1] + max_steps + 1) // self.ps)
+        # (device steps widen the table for max_steps more tokens before capture)
+        width = -(-prefix_tokens // self.ps) + own_max + (-(-max_steps // self.ps) + 2 if device_steps else 0)
         pool = int(math.ceil(1.25 * (-(-prefix_tokens // self.ps) + batch * own_max))) + batch
         self.mgr = AutoKVCacheManager(layers, hkv, d, dtype=dtype, device=self.device,
                                       total_gpu_mem_bytes=pool * layers * self.page_bytes, mem_utilization=1.0,
-                                      max_pages_per_seq=-(-prefix_tokens // self.ps) + own_max,
+                                      max_pages_per_seq=width,
                                       seq_lens=max(128, batch + 1))
         self.mgr.kv_cache.fill_(float("nan"))
         self.log: list = []
@@ -314,35 +320,61 @@ class SharedPrefixDecodeLoop:
     def begin_step(self) -> None:
         """Host bookkeeping and device metadata for one decode step (main.py:328-347)."""
         m = self.mgr
+        if self.device_steps:
+            with torch.cuda.stream(self.stream):
+                if m._dev is None:
+                    self._begin_device()
+                m.advance_device_step(self.batch)
+            if self.record:
+                for sid in self.ids:
+                    self._note(("append_tokens", sid, 1))
+                self._note(("fill_cuda_graph_metadata", self.batch, list(self.ids)))
+            return
         with torch.cuda.stream(self.stream):
             for sid in self.ids:
                 m.append_tokens(sid, 1)
                 self._note(("append_tokens", sid, 1))
             m.fill_cuda_graph_metadata(self.batch, self.ids)
             self._note(("fill_cuda_graph_metadata", self.batch, list(self.ids)))
-            self.wrapper.plan(m._cg_kv_indptr[self.batch], m._cg_kv_indices[self.batch],
-                              m._cg_kv_last_page_len[self.batch], self.hq, self.hkv, self.d, self.ps,
-                              pos_encoding_mode="NONE", q_data_type=self.dtype,
-                              kv_shared_pages=m._cg_kv_shared[self.batch] if self.shared_hint else None,
-                              cascade=self.cascade)
+            self._plan()
+
+    def _begin_device(self) -> None:
+        self.mgr.begin_device_steps(self.batch, self.ids, steps=self.max_steps)
+
+    def _plan(self) -> None:
+        m = self.mgr
+        self.wrapper.plan(m._cg_kv_indptr[self.batch], m._cg_kv_indices[self.batch],
+                          m._cg_kv_last_page_len[self.batch], self.hq, self.hkv, self.d, self.ps,
+                          pos_encoding_mode="NONE", q_data_type=self.dtype,
+                          kv_shared_pages=m._cg_kv_shared[self.batch] if self.shared_hint else None,
+                          cascade=self.cascade)
 
     def layers_fn(self) -> None:
-        """Every layer's append of the step's token and its decode (what the graph holds)."""
+        """Every layer's append of the step's token and its decode (what the graph holds); with
+        device steps, first the page-table step and the plan."""
         m = self.mgr
+        if self.device_steps:
+            m.device_step(self.batch)
+            self._plan()
         for layer in range(self.layers):
             m.append_paged_kv_cache_cuda_graph(self.k[layer], self.v[layer], self.batch, layer)
             self.wrapper.run(self.q[layer], m.kv_cache[layer], out=self.out[layer])
 
     def replay(self) -> None:
         """Run the step's layers from the captured graph (captured on the first call, after
-        an eager warm-up: a repeated append writes the same values to the same slots)."""
+        an eager warm-up: a repeated append writes the same values to the same slots; with
+        device steps there is no warm-up, since each run of the graph is a step)."""
         with torch.cuda.stream(self.stream):
             if self.graph is None:
-                self.layers_fn()
+                if not self.device_steps:
+                    self.layers_fn()
                 self.stream.synchronize()
                 self.graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(self.graph, stream=self.stream):
                     self.layers_fn()
+                self._table_ptr = self.mgr._table.data_ptr()
+            elif self.mgr._table.data_ptr() != self._table_ptr:
+                raise RuntimeError("the page table moved after the graph was captured")
             self.graph.replay()
 
     def retire(self) -> list:
@@ -353,6 +385,8 @@ class SharedPrefixDecodeLoop:
                 self.mgr.free(self.ids[r])
                 self._note(("free", self.ids[r]))
                 self.ids[r] = self._start_sequence()
+            if self.device_steps:  # the new batch goes back to the device (outside the step)
+                self._begin_device()
         return rows
 
     def new_inputs(self) -> None:

@@ -260,6 +260,29 @@ int pkv_pool_gather(const int32_t* table, int64_t stride, int32_t rows, const in
                     int64_t max_total, const int32_t* positions, int32_t page_size, int32_t* slots,
                     int32_t* err, void* stream);
 
+/* One decode step of a fixed batch, entirely on the device: the serving loop's
+ * append_tokens(b, n_tokens) for every sequence of the batch, in batch order (ecahlang/main.py
+ * :328-335 -> manager.py:187-205), then fill_cuda_graph_metadata for the bucket
+ * (manager.py:228-253).  rows[i] is the table row of batch entry i, or -1 for a padding entry
+ * (one page from padding_row, last_page_len 1, position 0).  npages[row] and last_len[row] are
+ * the device's copies of each row's page count and last-page length, and *n_free the device's
+ * free-stack size: each row takes (last_len + n_tokens) / page_size pages from the top of the
+ * stack after the rows before it, exactly as the reference's loop pops them, and keeps
+ * (last_len + n_tokens) % page_size as its new last-page length.  Then kv_indptr[batch + 1],
+ * kv_last_page_len[batch], positions[batch] (each row's newest token), kv_indices (at most
+ * min(max_total, num_indices) entries) and slots[batch] are written as pkv_pool_gather writes
+ * them (desc[4 * batch] is scratch).  No extension of the reference: it is the same step with no
+ * host work, so the step can be captured in a graph with the model and replayed.  A row whose
+ * pages the stack or its table row cannot hold is left unchanged, as are the rows after it, and
+ * *err is bumped: callers check the pool before they enqueue the step (AutoKVCacheManager does,
+ * and takes the reference's path, which raises, when it would run dry). */
+int pkv_pool_step(int32_t* stack, int32_t* n_free, int32_t* table, int64_t stride, int32_t rows_total,
+                  const int32_t* rows, int32_t batch, int32_t n_tokens, int32_t page_size,
+                  int32_t* npages, int32_t* last_len, int32_t padding_row, int32_t* desc,
+                  int32_t* kv_indptr, int32_t* kv_last_page_len, int32_t* positions,
+                  int32_t* kv_indices, int64_t num_indices, int64_t max_total, int32_t* slots,
+                  int32_t* err, void* stream);
+
 /* Top-k / top-p sampling from logits (flashinfer.sampling.top_k_top_p_sampling_from_logits at
  * ecahlang/main.py:377-379, 400-402, 489-491, 582-584: top-k first, then top-p on the
  * renormalised top-k distribution, deterministic=True).  logits: rows x vocab (row stride in

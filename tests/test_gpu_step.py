@@ -52,13 +52,15 @@ def _check_layer(loop, layer, rows, idx, ptr, last):
         np.testing.assert_allclose(got, ref, atol=2e-3, rtol=1e-2, err_msg=f"layer {layer} row {r}")
 
 
-@pytest.mark.parametrize("hint,cascade", [(True, False), (False, False), (True, True)])
-def test_small_loop_matches_oracle_every_step(hint, cascade):
-    """With the manager's shared-prefix hint (the prefix's pages kept in L2), without it, and
-    with the cascade (the prefix read once per group)."""
+@pytest.mark.parametrize("hint,cascade,device_steps", [(True, False, False), (False, False, False),
+                                                       (True, True, False), (True, False, True)])
+def test_small_loop_matches_oracle_every_step(hint, cascade, device_steps):
+    """With the manager's shared-prefix hint (the prefix's pages kept in L2), without it, with
+    the cascade (the prefix read once per group), and with the whole step in the graph (the
+    page-table step on the device)."""
     loop = workloads.SharedPrefixDecodeLoop(DEV, layers=3, batch=16, prefix_tokens=256, suffix=(1, 200),
                                             finish=4, max_steps=12, seed=7, record=True,
-                                            shared_hint=hint, cascade=cascade)
+                                            shared_hint=hint, cascade=cascade, device_steps=device_steps)
     ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
     done = 0
     for step in range(8):
@@ -85,10 +87,11 @@ def test_small_loop_matches_oracle_every_step(hint, cascade):
     assert loop.mgr.pool_errors() == 0
 
 
-def test_full_size_step_qwen_36_layers():
+@pytest.mark.parametrize("device_steps", [False, True])
+def test_full_size_step_qwen_36_layers(device_steps):
     """Qwen2.5-3B attention shape, 36 layers, batch 128, 2048-token shared prefix: three steps
     (the graph captured on the first), then layers 0, 17 and 35 checked on 8 sequences."""
-    loop = workloads.SharedPrefixDecodeLoop(DEV, max_steps=6, record=True)
+    loop = workloads.SharedPrefixDecodeLoop(DEV, max_steps=6, record=True, device_steps=device_steps)
     ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
     done = 0
     for step in range(3):

@@ -26,6 +26,7 @@ def _mirror(ref: RefKVCacheManager) -> AutoKVCacheManager:
     m._n_padding = len(ref.padding_pages)
     m._rows = ref.seq_lens + 1
     m._shared = dict(ref.shared)
+    m._dev = None
     m._staging = _HostStaging()
     return m
 
