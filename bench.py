@@ -365,6 +365,92 @@ def rope_append(args, torch, workloads, ops, dev):
     print(json.dumps(result), flush=True)
 
 
+def bulk_append(args, torch, workloads, ops, dev):
+    """append_paged_kv_cache (the reference's append, ecahlang/manager.py:153-185) of large
+    token batches at Qwen2.5-3B shape (2 KV heads, head_dim 128, fp16): 8 requests x 512
+    tokens (nnz 4096) and 128 requests x 512 tokens (nnz 65536), each onto a prefix of
+    U[0, 4096] tokens, pages scattered over the pool.  Bytes per token: K and V rows read and
+    written (4 * Hkv * D * 2) plus the token's batch index and position and its page-table
+    entry (12)."""
+    import numpy as np
+    from oracle import kv_ref
+    stream = torch.cuda.Stream(device=dev)
+    res = {}
+    for requests in (8, 128):
+        g = torch.Generator().manual_seed(4000 + requests)
+        prefix = torch.randint(0, 4097, (requests,), generator=g).tolist()
+        wb = workloads.build_batch([p + 512 for p in prefix], [512] * requests, 16, 2, 128, torch.float16,
+                                   seed=4100 + requests, fill_old=False)
+        nnz = wb.k_new.shape[0]
+        print(f"bench: bulk append, nnz {nnz}", file=sys.stderr, flush=True)
+        dv = wb.to(dev)
+
+        def app():
+            ops.append_paged_kv_cache(dv.k_new, dv.v_new, dv.batch_indices, dv.positions, dv.cache,
+                                      dv.indices, dv.indptr, dv.last)
+
+        with torch.cuda.stream(stream):
+            app()
+        torch.cuda.synchronize()
+        ok = None
+        if not args.no_check and requests == 8:  # bit-exact against the oracle on the whole pool
+            iv = lambda t: t.view(torch.int16).cpu().numpy()
+            want = kv_ref.append(iv(wb.cache), iv(wb.k_new), iv(wb.v_new), wb.batch_indices.numpy(),
+                                 wb.positions.numpy(), wb.indices.numpy(), wb.indptr.numpy(), 16)
+            ok = bool(np.array_equal(iv(dv.cache), want))
+        if args.profile_launches and requests == 128:
+            for _ in range(args.profile_launches):
+                app()
+            nb = append_bytes(wb) // 16 * 16
+            src = torch.empty(nb // 4, dtype=torch.int32, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            for _ in range(args.profile_launches):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            print(json.dumps({"profile_launches": args.profile_launches, "append_bytes": append_bytes(wb),
+                              "copy_bytes": nb}), flush=True)
+            return None
+        REP = 10
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(gr, stream=stream):
+                for _ in range(REP):
+                    app()
+        t = graph_time(torch, stream, gr, max(2, args.steps // (REP * 10)), REP)
+        nbytes = append_bytes(wb)
+        res[nnz] = dict(requests=requests, tokens=nnz, us=round(t * 1e6, 3), bytes=nbytes,
+                        gbs=round(nbytes / t / 1e9, 2), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                        parity_bitexact=ok)
+        del dv
+    big = res[max(res)]
+    # CPU baseline: the oracle append (numpy scatter) of 4096 tokens, median of 3
+    sb = workloads.build_batch([512] * 8, [512] * 8, 16, 2, 128, torch.float16, seed=3, fill_old=False)
+    iv = lambda t: t.view(torch.int16).numpy()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        kv_ref.append(iv(sb.cache), iv(sb.k_new), iv(sb.v_new), sb.batch_indices.numpy(), sb.positions.numpy(),
+                      sb.indices.numpy(), sb.indptr.numpy(), 16)
+        times.append(time.perf_counter() - t0)
+    result = {
+        "metric": "paged K/V append GB/s (% HBM peak), Qwen2.5-3B, 65536 tokens",
+        "value": big["gbs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) K/V rows, random page permutation, NaN-poisoned pool)",
+        "config": {"workload": "append_paged_kv_cache, 128 requests x 512 tokens (and 8 x 512) onto prefixes "
+                               "U[0, 4096], Hkv 2, D 128, page 16",
+                   "bytes_per_token": 4 * 2 * 128 * 2 + 12},
+        "by_nnz": {str(k): v for k, v in sorted(res.items())},
+        "roofline": {"bound": "hbm", "achieved": big["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": big["frac"], "traffic": None},
+        "cpu_baseline": {"value": round(append_bytes(sb) / statistics.median(times) / 1e9, 3), "unit": "GB/s",
+                         "cores": 1, "kind": "port",
+                         "sample": "4096 tokens: the oracle append (numpy scatter, which also copies its pool), median of 3",
+                         "cpu_model": cpu_model()},
+    }
+    print(json.dumps(result), flush=True)
+    return result
+
+
 def step36(args, torch, workloads, dev):
     """The 36-layer decode step at Qwen2.5-3B attention shape, batch 128, on a shared
     2048-token prefix (workloads.SharedPrefixDecodeLoop): per step, the page-table step
@@ -663,6 +749,7 @@ def main():
                     help="waves take pages on demand (faster, not bitwise reproducible)")
     ap.add_argument("--workload", default="qwen25_3b_b64",
                     choices=["qwen25_3b_b64", "llama31_8b_b128", "qwen25_3b_prefill", "qwen25_3b_step36",
+                             "qwen25_3b_bulk_append",
                              "qwen25_3b_sampling", "qwen25_3b_rope_append"],
                     help="qwen25_3b_b64: the headline decode + append step (default); llama31_8b_b128: "
                          "long-context decode at Llama-3.1-8B shape, B=128, ~4.4 GB of K/V in a 20 GB pool "
@@ -672,7 +759,8 @@ def main():
                          "2048-token prefix with pages allocated and freed by the device pool; "
                          "qwen25_3b_sampling: top-k/top-p sampling of 128 rows of the 151,936-token vocabulary; "
                          "qwen25_3b_rope_append: the model's rotary embedding fused with the append, "
-                         "4096-token prefill chunk and B=64 decode step, against the unfused sequence")
+                         "4096-token prefill chunk and B=64 decode step, against the unfused sequence; "
+                         "qwen25_3b_bulk_append: the plain append of 4096 and 65536 tokens")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="for counter runs: N eager decode and append launches, then N plain "
                          "copies of the decode's byte count (the counters' calibration), then exit")
@@ -699,6 +787,8 @@ def main():
         return sampling(args, torch, dev)
     if args.workload == "qwen25_3b_rope_append":
         return rope_append(args, torch, workloads, ops, dev)
+    if args.workload == "qwen25_3b_bulk_append":
+        return bulk_append(args, torch, workloads, ops, dev)
     print("bench: building Qwen2.5-3B B=64 decode batch", file=sys.stderr, flush=True)
     wb = workloads.qwen25_3b_decode()
     NL = args.layers

@@ -96,6 +96,10 @@ APPEND_CASES = {
     "llama31_8b_bf16_b8": lambda: workloads.build_batch([33, 1, 16, 17, 100, 2, 64, 5], [1] * 8,
                                                         32, 8, 128, torch.bfloat16, 44),
     "prefill_chunks_fp16": lambda: workloads.qwen25_3b_prefill(requests=4, chunk=64, max_prefix=300),
+    # rows of 32 and 64 chunks of 16 bytes: 2 and 1 tokens per wave, token counts that leave
+    # a partial last round
+    "hkv1_d128_fp16_37tok": lambda: workloads.build_batch([40, 3, 17], [30, 3, 4], 8, 1, 128, torch.float16, 45),
+    "hkv4_d64_bf16_23tok": lambda: workloads.build_batch([9, 50, 16], [6, 16, 1], 16, 4, 64, torch.bfloat16, 46),
 }
 
 
