@@ -18,6 +18,10 @@ Printed JSON line:
   cpu_baseline    the reference's CPU path (gather pages, then torch SDPA, in fp32) on this
                   host's cores, on the same batch
   ms_per_step     append + decode per step, over exactly --steps timed steps
+  extras          the other hot-path workloads, each at its own default size, summarised (its
+                  metric, value, roofline fraction, the times behind them, its CPU baseline):
+                  chunked prefill, long-context decode, the 36-layer shared-prefix step and the
+                  bulk append; --no-extras leaves them out, --workload <name> prints one in full
 
 roofline.traffic is the decode kernel's HBM bytes per launch measured with hardware counters
 (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over `bench.py --profile-launches N`, each
@@ -57,30 +61,50 @@ def append_bytes(wb) -> int:
 
 DECODE_SOURCES = ("decode.hip", "decode_mfma.hip", "decode_plan.hip", "decode_sched.h", "attn_common.h",
                   "mfma_common.h", "common.h")
+APPEND_SOURCES = ("append.hip", "common.h")
+APPEND_TRAFFIC_FILE = os.path.join(os.path.dirname(TRAFFIC_FILE), "append_traffic.json")
 
 
-def decode_source_hash() -> str:
-    """SHA-256 over the matrix-core decode path's sources (the kernel, its schedule and the
-    shared headers), so a counter record is only used for the code it was taken on."""
+def source_hash(names=DECODE_SOURCES) -> str:
+    """SHA-256 over a kernel's sources (for the decode: the kernel, its schedule and the shared
+    headers), so a counter record is only used for the code it was taken on."""
     import hashlib
     h = hashlib.sha256()
     root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ecahlang_amd", "csrc")
-    for name in DECODE_SOURCES:
+    for name in names:
         with open(os.path.join(root, name), "rb") as f:
             h.update(name.encode() + b"\0" + f.read())
     return h.hexdigest()
 
 
+def decode_source_hash() -> str:
+    return source_hash(DECODE_SOURCES)
+
+
+def _traffic_record(path):
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
 def measured_traffic(wb, w):
     """HBM bytes per decode launch from the committed counter runs, when they were taken on
     this workload, this workgroup count and these decode sources (None otherwise)."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-    except (OSError, ValueError):
-        return None
+    t = _traffic_record(TRAFFIC_FILE)
     if (t.get("decode_bytes") != decode_bytes(wb) or t.get("decode_ctas") != w._ctas
             or t.get("decode_source_sha256") != decode_source_hash()):
+        return None
+    return t.get("traffic_bytes")
+
+
+def measured_append_traffic(wb):
+    """HBM bytes per append launch from the committed counter runs (rocprofv3 FETCH_SIZE and
+    WRITE_SIZE over `--workload qwen25_3b_bulk_append --profile-launches N`, scaled by a copy
+    of the same byte count), when taken on this token batch and these append sources."""
+    t = _traffic_record(APPEND_TRAFFIC_FILE)
+    if t.get("append_bytes") != append_bytes(wb) or t.get("append_source_sha256") != source_hash(APPEND_SOURCES):
         return None
     return t.get("traffic_bytes")
 
@@ -172,7 +196,7 @@ def long_context(args, torch, workloads, Wrapper, dev):
                          "sample": f"4 median-length sequences ({sum(int(lens[b]) for b in sample)} tokens): "
                                    "gather + fp32 SDPA, median of 3", "cpu_model": cpu_model()},
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
@@ -259,7 +283,7 @@ def sampling(args, torch, dev):
                          "sample": "8 rows: torch softmax + topk + cumsum nucleus + multinomial, median of 3",
                          "cpu_model": cpu_model()},
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def rope_bytes(hq, hkv, d, es) -> int:
@@ -362,7 +386,7 @@ def rope_append(args, torch, workloads, ops, dev):
                                    "(which also copies its 40-page pool), median of 3",
                          "cpu_model": cpu_model()},
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def bulk_append(args, torch, workloads, ops, dev):
@@ -389,6 +413,7 @@ def bulk_append(args, torch, workloads, ops, dev):
             ops.append_paged_kv_cache(dv.k_new, dv.v_new, dv.batch_indices, dv.positions, dv.cache,
                                       dv.indices, dv.indptr, dv.last)
 
+        before = None if args.no_check or requests == 8 else dv.cache.clone()
         with torch.cuda.stream(stream):
             app()
         torch.cuda.synchronize()
@@ -398,6 +423,17 @@ def bulk_append(args, torch, workloads, ops, dev):
             want = kv_ref.append(iv(wb.cache), iv(wb.k_new), iv(wb.v_new), wb.batch_indices.numpy(),
                                  wb.positions.numpy(), wb.indices.numpy(), wb.indptr.numpy(), 16)
             ok = bool(np.array_equal(iv(dv.cache), want))
+        elif before is not None:
+            # bit-exact on the whole pool at full size: the pool before the launch with every
+            # token's K and V rows written at its page and slot by torch's index_put
+            ps = dv.cache.shape[2]
+            pos, bi = dv.positions.long(), dv.batch_indices.long()
+            page = dv.indices.long()[dv.indptr.long()[bi] + pos // ps]
+            slot = pos % ps
+            before[page, 0, slot] = dv.k_new
+            before[page, 1, slot] = dv.v_new
+            ok = bool(torch.equal(before.view(torch.int16), dv.cache.view(torch.int16)))
+            del before
         if args.profile_launches and requests == 128:
             for _ in range(args.profile_launches):
                 app()
@@ -418,6 +454,8 @@ def bulk_append(args, torch, workloads, ops, dev):
                     app()
         t = graph_time(torch, stream, gr, max(2, args.steps // (REP * 10)), REP)
         nbytes = append_bytes(wb)
+        if requests == 128:
+            traffic = measured_append_traffic(wb)
         res[nnz] = dict(requests=requests, tokens=nnz, us=round(t * 1e6, 3), bytes=nbytes,
                         gbs=round(nbytes / t / 1e9, 2), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
                         parity_bitexact=ok)
@@ -441,13 +479,12 @@ def bulk_append(args, torch, workloads, ops, dev):
                    "bytes_per_token": 4 * 2 * 128 * 2 + 12},
         "by_nnz": {str(k): v for k, v in sorted(res.items())},
         "roofline": {"bound": "hbm", "achieved": big["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": big["frac"], "traffic": None},
+                     "frac": big["frac"], "traffic": traffic},
         "cpu_baseline": {"value": round(append_bytes(sb) / statistics.median(times) / 1e9, 3), "unit": "GB/s",
                          "cores": 1, "kind": "port",
                          "sample": "4096 tokens: the oracle append (numpy scatter, which also copies its pool), median of 3",
                          "cpu_model": cpu_model()},
     }
-    print(json.dumps(result), flush=True)
     return result
 
 
@@ -550,7 +587,7 @@ def step36(args, torch, workloads, dev):
                          "sample": f"layer 0, 4 sequences ({sum(k.shape[0] for k in ks)} tokens): gather + fp32 SDPA, median of 3",
                          "cpu_model": cpu_model()},
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def step36_parity(loop, layers, nseq):
@@ -659,7 +696,7 @@ def chunked_prefill(args, torch, workloads, ops, dev):
                          "sample": f"request {b} ({qn} query rows over {L} keys): gather + fp32 causal SDPA, median of 3",
                          "cpu_model": cpu_model()},
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def cpu_model() -> str:
@@ -734,6 +771,38 @@ def parity(wb, out_dev):
     return {"max_abs_err": float(err.max()), "within_atol2e-3_rtol1e-2": ok}
 
 
+def extras(args, torch, runs):
+    """The other hot-path workloads, each run in this process at its own default size after the
+    headline's figures are taken, summarised as the line's "extras": chunked prefill (matrix-core
+    bound), long-context decode, the 36-layer shared-prefix step and the bulk append.  Each
+    entry carries that workload's own metric, value, roofline fraction and the times behind it;
+    `bench.py --workload <name>` prints its full line."""
+    sub = argparse.Namespace(**vars(args))
+    sub.profile_launches, sub.ctas = 0, None
+    keep = {
+        "qwen25_3b_prefill": ("prefill_us", "prefill_valu_us", "flops"),
+        "llama31_8b_b128": ("decode_us", "decode_bytes"),
+        "qwen25_3b_step36": ("step_ms", "graph_ms", "graph_unique_gbs", "parity"),
+        "qwen25_3b_bulk_append": ("by_nnz",),
+    }
+    out = {}
+    for name, fields in keep.items():
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        r = runs[name](sub)
+        e = {"metric": r["metric"], "value": r["value"], "unit": r["unit"],
+             "roofline_frac": r["roofline"]["frac"], "roofline_bound": r["roofline"]["bound"],
+             "traffic": r["roofline"]["traffic"]}
+        e.update({k: r[k] for k in fields})
+        if name == "qwen25_3b_step36":
+            e["device_steps"] = r["config"]["device_steps"]
+        if "cpu_baseline" in r:
+            e["cpu_baseline"] = {k: r["cpu_baseline"][k] for k in ("value", "unit", "cores", "kind")}
+        out[name] = e
+        print(f"bench: extras {name}: {e['value']} {e['unit']}", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -761,6 +830,8 @@ def main():
                          "qwen25_3b_rope_append: the model's rotary embedding fused with the append, "
                          "4096-token prefill chunk and B=64 decode step, against the unfused sequence; "
                          "qwen25_3b_bulk_append: the plain append of 4096 and 65536 tokens")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default workload only: skip the other workloads' summary (the line's 'extras')")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="for counter runs: N eager decode and append launches, then N plain "
                          "copies of the decode's byte count (the counters' calibration), then exit")
@@ -777,18 +848,26 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload == "llama31_8b_b128":
-        return long_context(args, torch, workloads, BatchDecodeWithPagedKVCacheWrapper, dev)
-    if args.workload == "qwen25_3b_prefill":
-        return chunked_prefill(args, torch, workloads, ops, dev)
-    if args.workload == "qwen25_3b_step36":
-        return step36(args, torch, workloads, dev)
-    if args.workload == "qwen25_3b_sampling":
-        return sampling(args, torch, dev)
-    if args.workload == "qwen25_3b_rope_append":
-        return rope_append(args, torch, workloads, ops, dev)
-    if args.workload == "qwen25_3b_bulk_append":
-        return bulk_append(args, torch, workloads, ops, dev)
+    runs = {
+        "qwen25_3b_b64": lambda a: headline(a, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, dev),
+        "llama31_8b_b128": lambda a: long_context(a, torch, workloads, BatchDecodeWithPagedKVCacheWrapper, dev),
+        "qwen25_3b_prefill": lambda a: chunked_prefill(a, torch, workloads, ops, dev),
+        "qwen25_3b_step36": lambda a: step36(a, torch, workloads, dev),
+        "qwen25_3b_sampling": lambda a: sampling(a, torch, dev),
+        "qwen25_3b_rope_append": lambda a: rope_append(a, torch, workloads, ops, dev),
+        "qwen25_3b_bulk_append": lambda a: bulk_append(a, torch, workloads, ops, dev),
+    }
+    result = runs[args.workload](args)
+    if result is None:  # --profile-launches: the counter run prints its own record
+        return
+    if args.workload == "qwen25_3b_b64" and not args.no_extras:
+        result["extras"] = extras(args, torch, runs)
+    print(json.dumps(result), flush=True)
+
+
+def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, dev):
+    """The default workload: append + decode of one Qwen2.5-3B layer at B = 64, rotated over
+    --layers pools (the module docstring describes the line it returns)."""
     print("bench: building Qwen2.5-3B B=64 decode batch", file=sys.stderr, flush=True)
     wb = workloads.qwen25_3b_decode()
     NL = args.layers
@@ -841,7 +920,7 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"profile_launches": n, "decode_bytes": decode_bytes(wb), "copy_bytes": nb}),
               flush=True)
-        return
+        return None
 
     stream = torch.cuda.Stream(device=dev)
 
@@ -934,7 +1013,7 @@ def main():
     if not args.no_cpu:
         print("bench: CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(wb)
-    print(json.dumps(result), flush=True)
+    return result
 
 
 if __name__ == "__main__":
