@@ -77,57 +77,166 @@ __device__ __forceinline__ bool resolve_dst(int64_t i, const int32_t* __restrict
   return ok;
 }
 
-// Tokens whose K and V rows together are CT <= 64 chunks of 16 bytes (CT dividing 64: e.g.
-// 2 heads of 128 fp16 dims = 64 chunks): each wave takes 64 / CT tokens at a time, lane l the
-// chunk l % CT of token l / CT (its k|v, head and offset fixed for the whole kernel), and U
-// such groups per round, so a wave has U tokens' source loads and page-table lookups in flight
-// at once.  The lanes of a token read the same metadata words: one request per token.  The
-// cache rows are written with non-temporal stores (nothing reads them back soon: the decode
-// that does copies them past the caches itself).  Measured at 65536 tokens of Qwen2.5-3B
-// shape: U = 2 with 8 workgroups of 4 waves per CU was the fastest of U = 1 .. 8 and 4 .. 64
-// workgroups per CU.
+// Tokens whose K and V rows together are CT = 64 / TPW chunks of 16 bytes (e.g. 2 heads of
+// 128 fp16 dims: CT = 64, TPW = 1): each wave moves TPW tokens at a time, lane l the chunk
+// l % CT of token l / CT (its k|v, head and offset fixed for the whole kernel), U such groups
+// per round.  A round's tokens are wave-uniform, so their page-table words are read with
+// scalar loads, which are counted apart from the vector loads and stores: the lookup chain
+// (batch index and position, then kv_indptr, then kv_indices) never waits for the rows in
+// flight.  The rounds are software-pipelined: the next round's source rows are requested
+// before this round's are stored, and the next round's lookups run while both are in flight.
+// The row loads and stores are issued as instructions of their own with the waits written
+// out (the compiler's counting would wait for every store before reusing its data registers);
+// the cache rows are written non-temporally (nothing reads them back soon: the decode that
+// does copies them past the caches itself).
 typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
-template <bool SLOTS, int U>
-__global__ __launch_bounds__(256) void append_tok_kernel(
+__device__ __forceinline__ u4v row_load(const char* p) {
+  u4v v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+  return v;
+}
+
+__device__ __forceinline__ void row_store_nt(char* p, u4v v) {
+  // (s_nop: a VALU write of the data registers right after a store of more than 8 bytes needs
+  // wait states the compiler does not count for an asm statement)
+  asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(p), "v"(v));
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding (they complete
+// in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+
+template <bool SLOTS, int U, int TPW>
+__global__ __launch_bounds__(256) void append_wave_kernel(
     const char* __restrict__ k, int64_t k_sn, int64_t k_sh, const char* __restrict__ v, int64_t v_sn,
     int64_t v_sh, const int32_t* __restrict__ bidx, const int32_t* __restrict__ pos, int32_t nnz,
     char* __restrict__ k_cache, char* __restrict__ v_cache, int64_t page_stride, int64_t num_pages,
     const int32_t* __restrict__ kv_indices, int64_t num_indices, const int32_t* __restrict__ kv_indptr,
     int32_t batch, int32_t hkv, int32_t row_bytes, int32_t ps, const int32_t* __restrict__ slots,
     int32_t* __restrict__ err) {
+  constexpr int CT = 64 / TPW, NT = U * TPW;  // chunks per token, tokens per wave round
   const int lane = threadIdx.x & 63;
-  const int cpr = row_bytes / 16, CT = 2 * hkv * cpr, tpw = 64 / CT;
-  const int t = lane / CT, c = lane - t * CT;          // token of the group, chunk of the token
-  const int kv = c / (hkv * cpr), rc = c - kv * hkv * cpr, h = rc / cpr, cc = rc - h * cpr;
+  const int t = lane / CT, c = lane % CT;
+  const int cpr = row_bytes / 16;
+  const int kv = c / (CT / 2), rc = c % (CT / 2), h = rc / cpr, cc = rc - h * cpr;
   const char* sbase = (kv ? v + h * v_sh : k + h * k_sh) + cc * 16;
   const int64_t ssn = kv ? v_sn : k_sn;
   char* dbase = (kv ? v_cache : k_cache) + (int64_t)h * row_bytes + cc * 16;
-  const int64_t per = (int64_t)tpw * U;                  // tokens per wave round
-  const int64_t gw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t base = gw * per; base < nnz; base += nw * per) {
-    uint4 val[U];
-    int64_t ii[U];
+  const int64_t slot_bytes = (int64_t)hkv * row_bytes;
+  const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  int64_t base = gw * NT;
+  if (base >= nnz) return;
+
+  // Source rows of the round starting at token b0.  Tokens past nnz read the last token's row
+  // (in bounds, never stored), so every round issues exactly U loads.
+  auto load = [&](int64_t b0, u4v (&val)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      ii[u] = base + (int64_t)u * tpw + t;
-      val[u] = ii[u] < nnz ? *reinterpret_cast<const uint4*>(sbase + ii[u] * ssn) : make_uint4(0, 0, 0, 0);
+      int64_t i = b0 + u * TPW + t;
+      i = i < nnz ? i : nnz - 1;
+      val[u] = row_load(sbase + i * ssn);
     }
-    asm volatile("" ::: "memory");  // every source load is issued before the lookups
+  };
+  // Destinations of the round's tokens (nullptr: past nnz, or metadata outside the sequence's
+  // pages, counted once per token, k|v and head, as the element-wise kernel counts).  Every lookup index is clamped into its array (the launch
+  // guarantees batch >= 1 and num_indices >= 1 without SLOTS), the checks are 32-bit and
+  // combined with & rather than &&, so each stage's NT scalar loads issue together with no
+  // branch between them.
+  const int npg = num_pages < INT32_MAX ? (int)num_pages : INT32_MAX;
+  const int nidx = num_indices < INT32_MAX ? (int)num_indices : INT32_MAX;
+  auto resolve = [&](int64_t b0, char* (&dst)[U]) {
+    const int64_t left = nnz - b0;  // tokens from b0 on (> 0)
+    int pg[NT], sl[NT];
+    bool in[NT], ok[NT];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (ii[u] >= nnz) continue;
-      int page, slot;
-      if (!resolve_dst<SLOTS>(ii[u], bidx, pos, slots, kv_indices, num_indices, kv_indptr, batch, num_pages,
-                              ps, page, slot)) {
-        if (cc == 0 && err) atomicAdd(err, 1);  // one count per token, k|v and head
-        continue;
+    for (int j = 0; j < NT; ++j) in[j] = j < left;
+    if constexpr (SLOTS) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) sl[j] = slots[__builtin_amdgcn_readfirstlane(in[j] ? (int)b0 + j : nnz - 1)];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        pg[j] = sl[j] / ps;
+        ok[j] = in[j] & (sl[j] >= 0) & (pg[j] < npg);
+        sl[j] -= pg[j] * ps;
       }
-      const u4v x = {val[u].x, val[u].y, val[u].z, val[u].w};
-      __builtin_nontemporal_store(x, reinterpret_cast<u4v*>(dbase + page * page_stride + (int64_t)slot * hkv * row_bytes));
+    } else {
+      int bi[NT], po[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        // (the index is wave-uniform; readfirstlane says so, so the loads go through the
+        // scalar cache)
+        const int i = __builtin_amdgcn_readfirstlane(in[j] ? (int)b0 + j : nnz - 1);
+        bi[j] = bidx[i];
+        po[j] = pos[i];
+      }
+      int lo[NT], hi[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        ok[j] = in[j] & (bi[j] >= 0) & (bi[j] < batch) & (po[j] >= 0);
+        bi[j] = ok[j] ? bi[j] : 0;
+        po[j] = ok[j] ? po[j] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < NT; ++j) lo[j] = kv_indptr[bi[j]], hi[j] = kv_indptr[bi[j] + 1];
+      int at[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int pi = po[j] / ps;
+        // lo + pi < hi <= INT32_MAX once pi < hi - lo (both counted from lo >= 0)
+        ok[j] = ok[j] & (lo[j] >= 0) & (pi < hi[j] - lo[j]);
+        ok[j] = ok[j] & (lo[j] + (ok[j] ? pi : 0) < nidx);
+        at[j] = ok[j] ? lo[j] + pi : 0;
+        sl[j] = po[j] - pi * ps;
+      }
+#pragma unroll
+      for (int j = 0; j < NT; ++j) pg[j] = kv_indices[at[j]];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) ok[j] = ok[j] & (pg[j] >= 0) & (pg[j] < npg);
     }
+    int bad = 0;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) bad += in[j] & !ok[j];
+    if (bad && lane == 0 && err) atomicAdd(err, bad * 2 * hkv);  // one count per token, k|v and head
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int p = pg[u * TPW], q = sl[u * TPW];
+      bool o = ok[u * TPW];
+#pragma unroll
+      for (int j = 1; j < TPW; ++j)
+        if (t == j) p = pg[u * TPW + j], q = sl[u * TPW + j], o = ok[u * TPW + j];
+      dst[u] = o ? dbase + p * page_stride + q * slot_bytes : nullptr;
+    }
+  };
+
+  // One round: request the next round's rows into `next`; wait until only those U loads are
+  // outstanding (this round's rows have arrived, and the previous round's stores, issued
+  // between the two, have completed); store this round's rows from `cur`; look up the next
+  // round's destinations.  Written out twice with the register sets swapped: the rows are
+  // never copied between registers while their loads are in flight.
+  u4v va[U], vb[U];
+  char* dst[U];
+  auto round = [&](u4v (&cur)[U], u4v (&next)[U]) {
+    const int64_t nb = base + nw * NT;
+    load(nb < nnz ? nb : base, next);  // (this round's rows again after the last round)
+    wait_vm<U>();
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (dst[u]) row_store_nt(dst[u], cur[u]);
+    if (nb >= nnz) return false;
+    resolve(nb, dst);
+    base = nb;
+    return true;
+  };
+  load(base, va);
+  resolve(base, dst);
+  while (round(va, vb) && round(vb, va)) {
   }
+  wait_vm<0>();  // the last loads (their rows unused) land before the wave ends
 }
 
 // One lane per VEC-byte chunk of a (token, k|v, head) row.  Index order, fastest first:
@@ -245,22 +354,33 @@ int launch_append(const void* append_key, int64_t k_stride_n, int64_t k_stride_h
   int blocks = (int)(want < 65536 ? want : 65536);
   hipStream_t s = (hipStream_t)stream;
   const int ct = vec == 16 ? 2 * num_kv_heads * (row_bytes / 16) : 0;
-  if (ct > 0 && ct <= 64 && 64 % ct == 0) {
+  if ((ct == 64 || ct == 32 || ct == 16 || ct == 8) && (slots || (batch >= 1 && num_indices >= 1))) {
+    // Measured at 65536 tokens of Qwen2.5-3B shape (CT = 64): U = 2 with at most 16
+    // workgroups of 4 waves per CU (22.0 us against 22.7 for U = 4 and 22.9 for U = 1; 4 and 8
+    // workgroups per CU were 0.9 and 0.3 us slower).
     constexpr int U = 2;
-    const int64_t per_wave = (int64_t)(64 / ct) * U, waves = (nnz + per_wave - 1) / per_wave;
+    const int tpw = 64 / ct;
+    const int64_t per_wave = (int64_t)tpw * U, waves = (nnz + per_wave - 1) / per_wave;
     int64_t nb = (waves + 3) / 4;  // 4 waves per block
-    const int64_t cap = 8 * (int64_t)num_cus(s);
+    const int64_t cap = 16 * (int64_t)num_cus(s);
     nb = nb < cap ? nb : cap;
-    if (slots)
-      hipLaunchKernelGGL((append_tok_kernel<true, U>), dim3((unsigned)nb), dim3(256), 0, s, (const char*)append_key,
-                         ksn, ksh, (const char*)append_value, vsn, vsh, batch_indices, positions, nnz,
-                         (char*)k_cache, (char*)v_cache, pstride, num_pages, kv_indices, num_indices, kv_indptr,
-                         batch, num_kv_heads, row_bytes, page_size, slots, err_count);
-    else
-      hipLaunchKernelGGL((append_tok_kernel<false, U>), dim3((unsigned)nb), dim3(256), 0, s, (const char*)append_key,
-                         ksn, ksh, (const char*)append_value, vsn, vsh, batch_indices, positions, nnz,
-                         (char*)k_cache, (char*)v_cache, pstride, num_pages, kv_indices, num_indices, kv_indptr,
-                         batch, num_kv_heads, row_bytes, page_size, slots, err_count);
+#define PKV_APPEND_WAVE(SL, T)                                                                        \
+  hipLaunchKernelGGL((append_wave_kernel<SL, U, T>), dim3((unsigned)nb), dim3(256), 0, s,             \
+                     (const char*)append_key, ksn, ksh, (const char*)append_value, vsn, vsh,          \
+                     batch_indices, positions, nnz, (char*)k_cache, (char*)v_cache, pstride,          \
+                     num_pages, kv_indices, num_indices, kv_indptr, batch, num_kv_heads, row_bytes,   \
+                     page_size, slots, err_count)
+    switch (tpw * 2 + (slots != nullptr)) {
+      case 2: PKV_APPEND_WAVE(false, 1); break;
+      case 3: PKV_APPEND_WAVE(true, 1); break;
+      case 4: PKV_APPEND_WAVE(false, 2); break;
+      case 5: PKV_APPEND_WAVE(true, 2); break;
+      case 8: PKV_APPEND_WAVE(false, 4); break;
+      case 9: PKV_APPEND_WAVE(true, 4); break;
+      case 16: PKV_APPEND_WAVE(false, 8); break;
+      default: PKV_APPEND_WAVE(true, 8); break;
+    }
+#undef PKV_APPEND_WAVE
     return (int)hipGetLastError();
   }
 #define PKV_APPEND(VB, SL)                                                                      \

@@ -100,6 +100,9 @@ APPEND_CASES = {
     # a partial last round
     "hkv1_d128_fp16_37tok": lambda: workloads.build_batch([40, 3, 17], [30, 3, 4], 8, 1, 128, torch.float16, 45),
     "hkv4_d64_bf16_23tok": lambda: workloads.build_batch([9, 50, 16], [6, 16, 1], 16, 4, 64, torch.bfloat16, 46),
+    # rows of 16 and 8 chunks: 4 and 8 tokens per wave
+    "hkv1_d64_fp16_29tok": lambda: workloads.build_batch([30, 7, 12], [20, 7, 2], 4, 1, 64, torch.float16, 47),
+    "hkv1_d32_bf16_45tok": lambda: workloads.build_batch([64, 21], [40, 5], 2, 1, 32, torch.bfloat16, 48),
 }
 
 
@@ -164,7 +167,47 @@ def test_append_out_of_range_metadata_is_skipped_and_counted():
                               dv.indices, dv.indptr, dv.last, err_count=err)
     torch.cuda.synchronize()
     assert np.array_equal(_bits(dv.cache), before)
-    assert err.item() > 0
+    assert err.item() == 2 * 2 * 2  # one count per token, K or V, and head
+
+
+def _index_put_append(cache, k, v, page, slot, keep):
+    """The append as torch's index_put on the device: the expected pool for large batches."""
+    want = cache.clone()
+    want[page[keep], 0, slot[keep]] = k[keep]
+    want[page[keep], 1, slot[keep]] = v[keep]
+    return want
+
+
+@pytest.mark.parametrize("by_slot", [False, True])
+def test_append_many_rounds_per_wave_with_bad_tokens(by_slot):
+    """40960 tokens (several pipelined rounds per wave at one workgroup per 8th of a CU's
+    slots), with tokens whose metadata is out of range scattered through the batch: every
+    other token lands bit for bit, the bad ones are skipped and counted."""
+    wb = workloads.build_batch([512] * 80, [512] * 80, 2, 2, 128, torch.float16, 49, fill_old=False)
+    dv = wb.to(DEV)
+    nnz, ps = dv.k_new.shape[0], wb.ps
+    bidx, pos = dv.batch_indices.clone(), dv.positions.clone()
+    page = dv.indices.long()[dv.indptr.long()[bidx.long()] + pos.long() // ps]
+    slot = pos.long() % ps
+    keep = torch.ones(nnz, dtype=torch.bool, device=DEV)
+    bad = [0, 777, 12345, 40959]
+    keep[bad] = False
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    want = _index_put_append(dv.cache, dv.k_new, dv.v_new, page, slot, keep)
+    if by_slot:
+        slots = (page * ps + slot).to(torch.int32)
+        slots[0], slots[777], slots[12345], slots[40959] = -1, wb.num_pages * ps, -16, 2 ** 31 - 1
+        ops.append_paged_kv_cache_slots(dv.k_new, dv.v_new, slots, dv.cache, err_count=err)
+    else:
+        pos[0] = 10 ** 6      # past the sequence's pages
+        bidx[777] = wb.batch  # no such sequence
+        bidx[12345] = -1
+        pos[40959] = -2
+        ops.append_paged_kv_cache(dv.k_new, dv.v_new, bidx, pos, dv.cache, dv.indices, dv.indptr, dv.last,
+                                  err_count=err)
+    torch.cuda.synchronize()
+    assert torch.equal(dv.cache.view(torch.int16), want.view(torch.int16))
+    assert err.item() == len(bad) * 2 * 2
 
 
 def _host_slots(wb):
