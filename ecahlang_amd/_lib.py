@@ -45,6 +45,11 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32,
          _f32, _i32, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp],
     ),
+    "pkv_batch_decode_append": (
+        _i32,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i32,
+         _i32, _i32, _i32, _i32, _f32, _i32, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp],
+    ),
     "pkv_batch_decode_noalloc": (
         _i32,
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32,

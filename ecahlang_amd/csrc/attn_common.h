@@ -45,6 +45,12 @@ struct DecodeParams {
   const int32_t* sched_pref;   // ... and its prefix item records
   int32_t cascade;             // the schedule was planned with prefix items
   int32_t r_cap;               // ranges the workspace holds
+  // Matrix-core kernel, append fused in (pkv_batch_decode_append): token b's new K and V rows
+  // (byte strides per token and head) belong at the last slot of sequence b's last page; null
+  // when the call appends nothing.
+  const char* ak;
+  const char* av;
+  int64_t ak_sn, ak_sh, av_sn, av_sh;
 };
 
 // A part_ml slot (one segment's (max, sum) pairs of every q head) spans whole 128-byte L2 lines,

@@ -3,6 +3,8 @@
 //   pkv_decode_workspace_bytes / pkv_decode_workspace_init / pkv_decode_plan
 //                                          <- BatchDecodeWithPagedKVCacheWrapper.plan
 //   pkv_batch_decode                       <- BatchDecodeWithPagedKVCacheWrapper.run
+//   pkv_batch_decode_append                <- the CUDA-graph decode step's append
+//                                             (ecahlang/manager.py:270-280) + run
 //   (ecahlang/main.py:203-204 construct, :341-347 / :444-455 plan, :68 run)
 //
 // Workspace (caller-owned bytes, 256-byte aligned regions; R = decode_ranges_cap ranges):
@@ -145,21 +147,81 @@ extern "C" int pkv_decode_uses_mfma(int32_t dtype, int32_t head_dim, int32_t num
              ? 1 : 0;
 }
 
-extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h,
-                                const void* k_cache, const void* v_cache, int64_t page_stride,
-                                int64_t num_pages, const int32_t* kv_indptr,
-                                const int32_t* kv_indices, int64_t num_indices,
-                                const int32_t* kv_last_page_len, int32_t batch,
-                                int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                                int32_t page_size, float sm_scale, int32_t num_ctas,
-                                void* workspace, int64_t workspace_bytes, void* out,
-                                int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
-                                int32_t flags, void* stream) {
+namespace {
+
+// New K and V rows of a decode step, one token per sequence (element strides).
+struct AppendRows {
+  const void* k;
+  int64_t k_sn, k_sh;
+  const void* v;
+  int64_t v_sn, v_sh;
+};
+
+// Token b's K and V rows at position seq_len_b - 1 = (n - 1) * ps + kv_last_page_len[b] - 1 of
+// sequence b's n listed pages: the append of a decode step (append_paged_kv_cache with
+// batch_indices = b, positions = seq_len_b - 1), one block per sequence, VT-sized pieces.  That
+// is the last page's slot kv_last_page_len - 1, or with kv_last_page_len 0 (the empty page the
+// pool adds when a page fills) the previous page's last slot.  A sequence whose page list is
+// empty or cut at num_indices, whose kv_last_page_len is outside [0, page_size], whose position
+// is negative or whose page id is outside the pool gets nothing (the matrix-core kernel's
+// fused append places and skips exactly the same tokens).
+template <typename VT>
+__global__ void append_last_kernel(AppendRows a, char* kc, char* vc, int64_t page_stride, int64_t num_pages,
+                                   const int32_t* __restrict__ indptr, const int32_t* __restrict__ indices,
+                                   int64_t num_indices, const int32_t* __restrict__ last, int32_t hkv,
+                                   int32_t row_bytes, int32_t ps) {
+  const int b = blockIdx.x;
+  const int e0 = indptr[b], e1 = indptr[b + 1], lp = last[b];
+  if (!(e0 >= 0 && e1 > e0 && (int64_t)e1 <= num_indices && lp >= 0 && lp <= ps)) return;
+  const int at = (e1 - e0 - 1) * ps + lp - 1;
+  if (at < 0) return;
+  const int page = indices[e0 + at / ps];
+  if (page < 0 || (int64_t)page >= num_pages) return;
+  const int per = row_bytes / (int)sizeof(VT);
+  const int64_t off = (int64_t)page * page_stride + (int64_t)(at % ps) * hkv * row_bytes;
+  for (int x = threadIdx.x; x < 2 * hkv * per; x += blockDim.x) {
+    const int kv = x / (hkv * per), r = x - kv * hkv * per, h = r / per, c = r - h * per;
+    const char* src = kv ? (const char*)a.v + b * a.v_sn + h * a.v_sh : (const char*)a.k + b * a.k_sn + h * a.k_sh;
+    char* dst = (kv ? vc : kc) + off + (int64_t)h * row_bytes;
+    *reinterpret_cast<VT*>(dst + c * sizeof(VT)) = *reinterpret_cast<const VT*>(src + c * sizeof(VT));
+  }
+}
+
+int launch_append_last(const AppendRows& a, int es, void* k_cache, void* v_cache, int64_t page_stride,
+                       int64_t num_pages, const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+                       const int32_t* last, int32_t batch, int32_t hkv, int32_t d, int32_t ps, hipStream_t s) {
+  AppendRows b = a;  // byte strides
+  b.k_sn *= es, b.k_sh *= es, b.v_sn *= es, b.v_sh *= es;
+  const int row = d * es;
+  const int64_t pstride = page_stride * es;
+  auto al = [&](int vec) {
+    const uintptr_t m = (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)k_cache | (uintptr_t)v_cache;
+    const int64_t st = b.k_sn | b.k_sh | b.v_sn | b.v_sh | pstride | row;
+    return m % vec == 0 && st % vec == 0;
+  };
+#define PKV_APPEND_LAST(VT)                                                                              \
+  hipLaunchKernelGGL(append_last_kernel<VT>, dim3(batch), dim3(128), 0, s, b, (char*)k_cache, (char*)v_cache, \
+                     pstride, num_pages, indptr, indices, num_indices, last, hkv, row, ps)
+  if (al(16)) PKV_APPEND_LAST(uint4);
+  else if (es == 4 || al(4)) PKV_APPEND_LAST(uint32_t);
+  else PKV_APPEND_LAST(uint16_t);
+#undef PKV_APPEND_LAST
+  return (int)hipGetLastError();
+}
+
+int batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, const AppendRows* app, void* k_cache,
+                 void* v_cache, int64_t page_stride, int64_t num_pages, const int32_t* kv_indptr,
+                 const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_last_page_len, int32_t batch,
+                 int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float sm_scale,
+                 int32_t num_ctas, void* workspace, int64_t workspace_bytes, void* out, int64_t o_stride_n,
+                 int64_t o_stride_h, int32_t dtype, int32_t flags, void* stream) {
   if (batch <= 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_ctas <= 0) return kBadArg;
   if (num_qo_heads % num_kv_heads) return kBadGroup;
   if (page_size <= 0) return kBadPageSize;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return kBadHeadDim;
   if (num_indices < 0 || num_pages < 0) return kBadArg;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kBadDType;
+  if (app && (!app->k || !app->v)) return kBadArg;
   if (!ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
   const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices, workspace_bytes);
   if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
@@ -192,13 +254,72 @@ extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_str
   const int es = dtype == kF32 ? 4 : 2;
   P.q_vec = ((uintptr_t)q % 16 == 0) && ((q_stride_n * es) % 16 == 0) && ((q_stride_h * es) % 16 == 0);
   P.o_vec = ((uintptr_t)out % 8 == 0) && ((o_stride_n * es) % 8 == 0) && ((o_stride_h * es) % 8 == 0);
+  P.ak = P.av = nullptr;
+  P.ak_sn = P.ak_sh = P.av_sn = P.av_sh = 0;
   hipStream_t s = (hipStream_t)stream;
   const int g = num_qo_heads / num_kv_heads;
   // The matrix-core kernel reads the schedule pkv_decode_plan wrote into this workspace.
   if ((flags & PKV_DECODE_PLANNED) && !(flags & PKV_DECODE_VALU) && P.q_vec && page_size == 16 &&
-      decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch))
+      decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch)) {
+    if (app) {
+      // The append rides in the decode kernel (the wave that attends a sequence's last page
+      // writes the token there) for the fixed page order of a plain schedule and 16-byte rows;
+      // otherwise it is a launch of its own before the decode.
+      const uintptr_t m = (uintptr_t)app->k | (uintptr_t)app->v;
+      const int64_t st = (app->k_sn | app->k_sh | app->v_sn | app->v_sh) * es;
+      if (!P.dynamic && !P.cascade && m % 16 == 0 && st % 16 == 0) {
+        P.ak = (const char*)app->k;
+        P.av = (const char*)app->v;
+        P.ak_sn = app->k_sn * es, P.ak_sh = app->k_sh * es, P.av_sn = app->v_sn * es, P.av_sh = app->v_sh * es;
+      } else {
+        const int rc = launch_append_last(*app, es, k_cache, v_cache, page_stride, num_pages, kv_indptr, kv_indices,
+                                          num_indices, kv_last_page_len, batch, num_kv_heads, head_dim, page_size, s);
+        if (rc) return rc;
+      }
+    }
     return decode_mfma_dispatch(P, dtype, head_dim, s);
+  }
+  if (app) {
+    const int rc = launch_append_last(*app, es, k_cache, v_cache, page_stride, num_pages, kv_indptr, kv_indices,
+                                      num_indices, kv_last_page_len, batch, num_kv_heads, head_dim, page_size, s);
+    if (rc) return rc;
+  }
   return decode_valu_dispatch(P, dtype, head_dim, s);
+}
+
+}  // namespace
+
+extern "C" int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache, int64_t page_stride,
+                                int64_t num_pages, const int32_t* kv_indptr,
+                                const int32_t* kv_indices, int64_t num_indices,
+                                const int32_t* kv_last_page_len, int32_t batch,
+                                int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t page_size, float sm_scale, int32_t num_ctas,
+                                void* workspace, int64_t workspace_bytes, void* out,
+                                int64_t o_stride_n, int64_t o_stride_h, int32_t dtype,
+                                int32_t flags, void* stream) {
+  return batch_decode(q, q_stride_n, q_stride_h, nullptr, const_cast<void*>(k_cache), const_cast<void*>(v_cache),
+                      page_stride, num_pages, kv_indptr, kv_indices, num_indices, kv_last_page_len, batch,
+                      num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, num_ctas, workspace,
+                      workspace_bytes, out, o_stride_n, o_stride_h, dtype, flags, stream);
+}
+
+extern "C" int pkv_batch_decode_append(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                       const void* append_key, int64_t k_stride_n, int64_t k_stride_h,
+                                       const void* append_value, int64_t v_stride_n, int64_t v_stride_h,
+                                       void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
+                                       const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
+                                       const int32_t* kv_last_page_len, int32_t batch, int32_t num_qo_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float sm_scale,
+                                       int32_t num_ctas, void* workspace, int64_t workspace_bytes, void* out,
+                                       int64_t o_stride_n, int64_t o_stride_h, int32_t dtype, int32_t flags,
+                                       void* stream) {
+  const AppendRows app{append_key, k_stride_n, k_stride_h, append_value, v_stride_n, v_stride_h};
+  return batch_decode(q, q_stride_n, q_stride_h, &app, k_cache, v_cache, page_stride, num_pages, kv_indptr,
+                      kv_indices, num_indices, kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
+                      page_size, sm_scale, num_ctas, workspace, workspace_bytes, out, o_stride_n, o_stride_h, dtype,
+                      flags, stream);
 }
 
 // ---- allocation-free variant: the workspace is a file-scope device array

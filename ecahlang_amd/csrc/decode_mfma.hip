@@ -98,6 +98,7 @@ __device__ __forceinline__ f4 fold_copies(int J, F&& copy) {
 
 struct Seg {
   int b, beg, end, nv, slot0, part, nparts, np;
+  int app_page, app_row;  // range page and row of the step's new token (-1: not in this segment)
 };
 // A segment word (decode_sched.h), clamped so that a stale or malformed schedule cannot index
 // past the batch, the record or the partial slots.
@@ -108,10 +109,14 @@ __device__ __forceinline__ Seg unpack_seg(int4 v, int len, int batch, int slot_c
   const int nv = (int)(((unsigned)v.x >> kSegBBits) & 31);
   s.nv = nv > 16 ? 16 : nv;
   s.np = (int)((unsigned)v.x >> (kSegBBits + 5));
-  s.beg = v.y & 0xFFFF;
+  s.beg = v.y & 0x3FF;
   s.end = (v.y >> 16) & 0xFFFF;
   s.end = s.end > len ? len : s.end;
   s.beg = s.beg > s.end ? s.end : s.beg;
+  const int app = (v.y >> 10) & 63;
+  s.app_page = app ? s.end - 1 - ((app - 1) >> 4) : -1;
+  s.app_page = s.app_page >= s.beg ? s.app_page : -1;
+  s.app_row = (app - 1) & 15;
   s.nparts = ((v.w >> 16) & 0xFFFF) + 1;
   s.nparts = s.nparts > slot_cap ? slot_cap : s.nparts;
   s.slot0 = v.z < 0 ? 0 : (v.z > slot_cap - s.nparts ? slot_cap - s.nparts : v.z);
@@ -541,6 +546,21 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     float m = -INFINITY, lsum = 0.f;
     auto start_segment = [&]() __attribute__((always_inline)) {
       sg = seg_at(si);
+      if constexpr (!CASC) {
+        // Fused append: the wave that will attend the page that receives the step's token
+        // (range page k goes to rank k % J) copies the token's K and V rows of its head block
+        // into its 1 KB of the exchange buffer now (lane l's 16 bytes at byte 16 l: K chunks,
+        // then V chunks), so they have landed when that page comes up.  The buffer is free
+        // until this segment's end: exchanges write it only there.
+        if (P.ak && active && sg.app_page >= 0 && sg.app_page % J == j) {
+          const int c = lane % (2 * CPR), cc = c % CPR;
+          const bool isv = c >= CPR;
+          const int64_t h = (int64_t)hb * HB + cc / (D / 8);
+          const char* src = isv ? P.av + (int64_t)sg.b * P.av_sn + h * P.av_sh
+                                : P.ak + (int64_t)sg.b * P.ak_sn + h * P.ak_sh;
+          dma16(src + 16 * (cc % (D / 8)), reinterpret_cast<const char*>(&s_x[0][wave][0]));
+        }
+      }
       // query operand: column lr's query head, dims of its own KV head only
       uint4 qv[KSH];
       if (si < qs) {
@@ -663,6 +683,26 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       }
       // K of unit pi has landed (its V may still be in flight)
       wait_vm<NI>();
+      if constexpr (!CASC) {
+        // Fused append at the page that receives the step's token: once the page's V and the
+        // new rows (copied at the segment's start) have landed, the rows replace their row of
+        // the staged K and V tiles and are written to that slot of the page in the cache.
+        if (P.ak && pi == sg.app_page) {
+          wait_vm<0>();
+          if (lane < 2 * CPR) {
+            const bool isv = lane >= CPR;
+            const int c = lane - (isv ? CPR : 0), r = sg.app_row;
+            const uint4 x = *reinterpret_cast<const uint4*>(&s_x[0][wave][lane]);
+            char* tile = isv ? vbuf : kbuf;
+            *reinterpret_cast<uint4*>(tile + r * RB + ((c ^ (isv ? vx<RB>(r) : kx<RB>(r))) << 4)) = x;
+            if (page_ok(cpid)) {
+              T* dst = const_cast<T*>(isv ? vc : kc) + (int64_t)cpid * P.page_stride + (r * rowstride32 + 8 * c) +
+                       hboff;
+              *reinterpret_cast<uint4*>(dst) = x;
+            }
+          }
+        }
+      }
       f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
       const char* krow = kbuf + lr * RB;
 #pragma unroll

@@ -401,14 +401,24 @@ __global__ __launch_bounds__(kRecThreads) void decode_plan_records_kernel(PlanPa
           const int idx = P.rank[b] - rf;
           const int beg = (pos > rs ? pos : rs) - rs, end = (pos + len < re ? pos + len : re) - rs;
           if (idx >= 0 && idx < kRangePages && end > beg && P.swin[b] >= 0) {
-            const int e1 = P.indptr[b + 1];
-            int nvl = P.last[b];
-            nvl = nvl < 0 ? 0 : (nvl > P.page_size ? P.page_size : nvl);
+            const int e0 = P.indptr[b], e1 = P.indptr[b + 1];
+            const int lp = P.last[b];
+            int nvl = lp < 0 ? 0 : (lp > P.page_size ? P.page_size : lp);
             // the segment's last page is the sequence's last page only if the list was not cut
             const int nv = (clip(e1) == e1 && pos + len <= re) ? nvl : P.page_size;
+            // the step's token: position (n - 1) * ps + last - 1 of the sequence's n listed
+            // pages (an uncut list, 0 <= last <= ps), whose pages are the suffix's last len
+            int app = 0;
+            const int n = e1 - e0;
+            const int at = (n - 1) * P.page_size + lp - 1;
+            if (clip(e1) == e1 && e0 >= 0 && n >= 1 && lp >= 0 && lp <= P.page_size && at >= 0) {
+              const int k = pos + (at / P.page_size - (n - len)) - rs;  // range page of the token
+              const int back = end - 1 - k;
+              if (k >= beg && k < end && back <= 1) app = 1 + ((back << 4) | (at % P.page_size));
+            }
             int zlo;
             const int np = parts_of(b, &zlo);
-            const int4 sg = make_int4(seg_pack_b(b, nv, P.npb[b]), beg | (end << 16), P.sbase[b],
+            const int4 sg = make_int4(seg_pack_b(b, nv, P.npb[b]), seg_pack_range(beg, end, app), P.sbase[b],
                                       seg_pack_part(P.npb[b] + P.nzb[w] - zlo, np));
             *reinterpret_cast<int4*>(rec + kRecSegOff + 4 * idx) = sg;
             if (idx < kHeadSegs) *reinterpret_cast<int4*>(head + kRecSegOff + 4 * idx) = sg;

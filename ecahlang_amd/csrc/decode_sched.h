@@ -6,11 +6,15 @@
 // num_indices), minus the shared prefix pages described below, is cut into R ranges of equal
 // weight; each range gets one fixed-size record:
 //   header   [len, nseg, R, prefix, ...]                 kRecHdr int32 (in the range's head)
-//   segments nseg x int4 {b | nv << 22 | np << 27, beg | end << 16, slot0,
+//   segments nseg x int4 {b | nv << 22 | np << 27, beg | app << 10 | end << 16, slot0,
 //                         part | (nparts - 1) << 16}
 //            one per sequence with pages in the range: range pages [beg, end) are sequence
 //            b's, nv is the valid token count of the segment's last page (16 unless that page
-//            is the sequence's last).  The sequence's softmax state is cut into nparts parts
+//            is the sequence's last).  app (bits 10-15 of the second word, 0: none) places the
+//            decode step's new token when it falls in this segment: at position
+//            (pages - 1) * page_size + kv_last_page_len - 1 of the sequence, i.e. range page
+//            end - 1 - ((app - 1) >> 4), row (app - 1) & 15 (the page before an empty last page
+//            when kv_last_page_len is 0).  The sequence's softmax state is cut into nparts parts
 //            whose partials live in slots slot0 .. slot0 + nparts - 1; this segment is part
 //            `part` (nparts == 1: the segment is the whole sequence and writes the output).
 //            The first np parts are shared-prefix chunks, each written by Hkv prefix items
@@ -85,6 +89,7 @@ constexpr int kPrefixCostNum = 1, kPrefixCostDen = 1;
 
 // Segment word packing.
 constexpr int kSegBBits = 22;
+__host__ __device__ inline int seg_pack_range(int beg, int end, int app) { return beg | (app << 10) | (end << 16); }
 __host__ __device__ inline int seg_pack_b(int b, int nv, int np) {
   return (int)((unsigned)b | ((unsigned)nv << kSegBBits) | ((unsigned)np << (kSegBBits + 5)));
 }

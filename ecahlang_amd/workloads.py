@@ -229,11 +229,13 @@ class SharedPrefixDecodeLoop:
     the prefix once per group of sequences instead.  With ``device_steps`` the step's
     append_tokens and metadata run on the device (AutoKVCacheManager.begin_device_steps) and the
     graph holds the whole step: page-table step, plan, and every layer's append + decode; the
-    host's per-step work is ``advance_device_step``."""
+    host's per-step work is ``advance_device_step``.  With ``fused_append`` (the default) each
+    layer's append rides in its decode launch (``run(..., append_kv=)``); without it the append
+    is a launch of its own through the bucket's slots, as the reference's step makes it."""
 
     def __init__(self, device, *, layers=36, batch=128, hq=16, hkv=2, d=128, dtype=torch.float16,
                  prefix_tokens=2048, suffix=(64, 1024), finish=8, max_steps=64, seed=1005, scale=0.5,
-                 record=False, shared_hint=True, cascade=False, device_steps=False):
+                 record=False, shared_hint=True, cascade=False, device_steps=False, fused_append=True):
         from .manager import AutoKVCacheManager
         from .wrappers import BatchDecodeWithPagedKVCacheWrapper
 
@@ -241,7 +243,7 @@ class SharedPrefixDecodeLoop:
         self.layers, self.batch, self.hq, self.hkv, self.d, self.dtype = layers, batch, hq, hkv, d, dtype
         self.ps = 16
         self.prefix_tokens, self.suffix, self.finish, self.scale = prefix_tokens, suffix, finish, scale
-        self.shared_hint, self.cascade = shared_hint, cascade
+        self.shared_hint, self.cascade, self.fused_append = shared_hint, cascade, fused_append
         self.device_steps, self.max_steps = device_steps, max_steps
         self.gen = torch.Generator().manual_seed(seed + 7919)
         self.dgen = torch.Generator(device=self.device).manual_seed(seed)
@@ -357,8 +359,12 @@ class SharedPrefixDecodeLoop:
             m.device_step(self.batch)
             self._plan()
         for layer in range(self.layers):
-            m.append_paged_kv_cache_cuda_graph(self.k[layer], self.v[layer], self.batch, layer)
-            self.wrapper.run(self.q[layer], m.kv_cache[layer], out=self.out[layer])
+            if self.fused_append:
+                self.wrapper.run(self.q[layer], m.kv_cache[layer], out=self.out[layer],
+                                 append_kv=(self.k[layer], self.v[layer]))
+            else:
+                m.append_paged_kv_cache_cuda_graph(self.k[layer], self.v[layer], self.batch, layer)
+                self.wrapper.run(self.q[layer], m.kv_cache[layer], out=self.out[layer])
 
     def replay(self) -> None:
         """Run the step's layers from the captured graph (captured on the first call, after

@@ -158,7 +158,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, q_scale=None, k_scale=None,
             v_scale=None, out: torch.Tensor | None = None, lse=None, return_lse: bool = False,
-            window_left=None, enable_pdl=None, force_valu: bool = False) -> torch.Tensor:
+            window_left=None, enable_pdl=None, force_valu: bool = False, append_kv=None) -> torch.Tensor:
+        """FlashInfer's run (ecahlang/main.py:68).  Extension: ``append_kv=(k, v)``, each
+        [batch, num_kv_heads, head_dim] with unit inner stride, first appends token b's rows at
+        position seq_len_b - 1 (the decode step's append through the CUDA-graph metadata,
+        ecahlang/manager.py:270-280) -- in the same launch on the matrix-core path."""
         if not self._planned:
             raise RuntimeError("plan() must be called before run()")
         if return_lse or lse is not None:
@@ -176,6 +180,23 @@ class BatchDecodeWithPagedKVCacheWrapper:
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
             raise ValueError("out must match q's shape and dtype")
+        if append_kv is not None:
+            k, v = append_kv
+            for t, n in ((k, "k"), (v, "v")):
+                if t.shape != (self._batch, self._hkv, self._d) or t.stride(2) != 1 or t.dtype != self._q_dtype:
+                    raise ValueError(f"append {n} must be [{self._batch}, {self._hkv}, {self._d}] "
+                                     f"{self._q_dtype} with unit inner stride")
+            check(lib().pkv_batch_decode_append(
+                q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+                v.data_ptr(), v.stride(0), v.stride(1), cv.k_ptr, cv.v_ptr, cv.page_stride, cv.num_pages,
+                self._indptr.data_ptr(), self._indices.data_ptr(), self._indices.numel(),
+                self._last.data_ptr(), self._batch,
+                self._hq, self._hkv, self._d, self._ps, self._sm_scale, self._ctas,
+                self._workspace.data_ptr(), self._workspace.numel() * self._workspace.element_size(),
+                out.data_ptr(), out.stride(0), out.stride(1), dtype_code(q.dtype),
+                self._flags | (_DECODE_VALU if force_valu else 0),
+                stream_ptr(q.device)), "BatchDecodeWithPagedKVCacheWrapper.run(append_kv=)")
+            return out
         check(lib().pkv_batch_decode(
             q.data_ptr(), q.stride(0), q.stride(1), cv.k_ptr, cv.v_ptr, cv.page_stride, cv.num_pages,
             self._indptr.data_ptr(), self._indices.data_ptr(), self._indices.numel(),

@@ -176,6 +176,31 @@ int pkv_batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, cons
                      int64_t workspace_bytes, void* out, int64_t o_stride_n, int64_t o_stride_h,
                      int32_t dtype, int32_t flags, void* stream);
 
+/* The CUDA-graph decode step's append (ecahlang/manager.py:270-280, append_paged_kv_cache
+ * through the bucket's metadata, whose positions are seq_len_b - 1: main.py:62-64) followed by
+ * BatchDecodeWithPagedKVCacheWrapper.run (main.py:68), in one call: token b's new K and V rows
+ * (append_key / append_value [batch, num_kv_heads, head_dim], element strides) go to position
+ * seq_len_b - 1 = (n_b - 1) * page_size + kv_last_page_len[b] - 1 of sequence b's n_b pages
+ * (the last page's slot kv_last_page_len - 1; with kv_last_page_len 0, the empty page the
+ * reference's append_tokens adds when a page fills, the previous page's last slot), then out
+ * is computed as by pkv_batch_decode over the caches holding them; out and the caches are
+ * bitwise those of pkv_append_paged_kv_cache at those positions + pkv_batch_decode.  A sequence
+ * whose page list is empty or cut at num_indices, whose kv_last_page_len is outside
+ * [0, page_size], whose position is negative or whose page id is outside the pool gets no
+ * append.  On the matrix-core kernel (PKV_DECODE_PLANNED, no
+ * PKV_DECODE_DYNAMIC, a plan without PKV_PLAN_CASCADE, 16-byte aligned rows) the append rides
+ * in the decode launch; otherwise it is a launch of its own before the decode. */
+int pkv_batch_decode_append(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                            const void* append_key, int64_t k_stride_n, int64_t k_stride_h,
+                            const void* append_value, int64_t v_stride_n, int64_t v_stride_h,
+                            void* k_cache, void* v_cache, int64_t page_stride, int64_t num_pages,
+                            const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
+                            const int32_t* kv_last_page_len, int32_t batch, int32_t num_qo_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float sm_scale,
+                            int32_t num_ctas, void* workspace, int64_t workspace_bytes, void* out,
+                            int64_t o_stride_n, int64_t o_stride_h, int32_t dtype, int32_t flags,
+                            void* stream);
+
 /* pkv_decode_plan + pkv_batch_decode in one call that allocates nothing and takes no workspace:
  * the counters, split partials and schedule live in a file-scope device array of
  * PKV_NOALLOC_SCRATCH_BYTES per device, held by every device the library runs on until the
