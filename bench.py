@@ -3,7 +3,8 @@
 Workload (default): one attention layer at Qwen2.5-3B shape (16 q / 2 kv heads, head_dim 128,
 fp16), batch 64, contexts U[512, 4096], page_size 16, pages scattered by a seeded permutation
 over a pool 1.25x the pages used, values N(0,1)*0.5.  A step is one pass of the hot path over
-that batch: append one token per sequence into its page, then paged decode attention.
+that batch: append one token per sequence into its page, then paged decode attention (one
+launch: the decode kernel writes each token as it attends its page).
 
 Steps rotate over --layers independent layer pools (4 x ~200 MB) so every step streams its
 pages from HBM rather than from the 256 MB Infinity Cache.  Each layer's step is captured once
@@ -15,9 +16,12 @@ Printed JSON line:
                   decode launches; the median of 5 samples, each after a warm-up burst)
   roofline        the decode kernel against MI355X's 8 TB/s HBM peak
   append_mtok_s   appended tokens per second of the append kernel (nnz = batch)
+  decode_append_fused_us  the decode launch with the step's append fused in (run(append_kv=):
+                  one launch where the reference's step makes two)
   cpu_baseline    the reference's CPU path (gather pages, then torch SDPA, in fp32) on this
                   host's cores, on the same batch
-  ms_per_step     append + decode per step, over exactly --steps timed steps
+  ms_per_step     append + decode per step (one launch, the append fused in), over exactly
+                  --steps timed steps
   extras          the other hot-path workloads, each at its own default size, summarised (its
                   metric, value, roofline fraction, the times behind them, its CPU baseline):
                   chunked prefill, long-context decode, the 36-layer shared-prefix step and the
@@ -491,18 +495,21 @@ def bulk_append(args, torch, workloads, ops, dev):
 def step36(args, torch, workloads, dev):
     """The 36-layer decode step at Qwen2.5-3B attention shape, batch 128, on a shared
     2048-token prefix (workloads.SharedPrefixDecodeLoop): per step, the page-table step
-    (append_tokens for every sequence, fill_cuda_graph_metadata), the plan, and 36 x (append +
-    decode).  By default the whole step is one graph replay and the host's part is
+    (append_tokens for every sequence, fill_cuda_graph_metadata), the plan, and 36 decodes, each
+    with the layer's append of the step's token fused in (the reference's step makes each append
+    a launch of its own).  By default the whole step is one graph replay and the host's part is
     advance_device_step (AutoKVCacheManager.begin_device_steps); with --host-steps the
     bookkeeping runs on the host per step, as the reference's loop does, and the graph holds
     the layers only.  The timed region of each step runs from before the host's part to the
     end of the replay; retiring 8 sequences and writing their successors' tokens (the work of
-    a prefill) happens between timed regions."""
+    a prefill) happens between timed regions.  graph_ms times the replay alone on alternate
+    steps (their host part done before the first event); graph_back_to_back_ms replays the
+    graph with the host enqueueing ahead."""
     import numpy as np
     steps, warmup = max(1, min(args.steps, 40)), max(1, min(args.warmup, 4))
     print("bench: building the 36-layer shared-prefix decode loop (B=128)", file=sys.stderr, flush=True)
     device_steps = not args.host_steps
-    loop = workloads.SharedPrefixDecodeLoop(dev, max_steps=steps + warmup + 2, device_steps=device_steps)
+    loop = workloads.SharedPrefixDecodeLoop(dev, max_steps=2 * steps + warmup + 2, device_steps=device_steps)
     for _ in range(warmup):
         loop.begin_step()
         loop.replay()
@@ -513,17 +520,26 @@ def step36(args, torch, workloads, dev):
     import gc
     gc.collect()
     gc.freeze()
-    times, byts = [], []
-    for _ in range(steps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(loop.stream)
-        loop.begin_step()
-        loop.replay()
-        e1.record(loop.stream)
-        e1.synchronize()
-        times.append(e0.elapsed_time(e1) / 1e3)
-        byts.append(loop.step_bytes())
-        loop.retire()
+    # Steps alternate between the timed step (host part, then replay) and the same kind of
+    # step with the host part done before the first event (the replay alone: graph_ms), so the
+    # two figures are taken on the same mix of batch states; each starts on an idle GPU.
+    times, gtimes, byts, gbyts = [], [], [], []
+    with loop.on_stream():
+        for i in range(2 * steps):
+            full = i % 2 == 0
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if not full:
+                loop.begin_step()
+            loop.stream.synchronize()
+            e0.record(loop.stream)
+            if full:
+                loop.begin_step()
+            loop.replay()
+            e1.record(loop.stream)
+            e1.synchronize()
+            (times if full else gtimes).append(e0.elapsed_time(e1) / 1e3)
+            (byts if full else gbyts).append(loop.step_bytes())
+            loop.retire()
     # parity on the last step's layers 0 and 35, 8 sequences each, before the next step
     par = None
     if not args.no_check:
@@ -531,16 +547,16 @@ def step36(args, torch, workloads, dev):
         loop.replay()
         torch.cuda.synchronize()
         par = step36_parity(loop, [0, loop.layers - 1], 8)
-    # the graph alone, replayed back to back (each replay repeats the same appends; with device
-    # steps each replay is one more step, whose pages the pool has room for: nothing reads the
-    # loop's state after this)
-    t_graph = graph_time(torch, loop.stream, loop.graph, 4, 1)
+    # the graph replayed back to back, the host enqueueing ahead (each replay repeats the same
+    # appends; with device steps each replay is one more step, whose pages the pool has room
+    # for: nothing reads the loop's state after this)
+    t_b2b = graph_time(torch, loop.stream, loop.graph, 4, 1)
     L = loop.layers
-    t_step = float(np.mean(times))
+    t_step, t_graph = float(np.mean(times)), float(np.mean(gtimes))
     uniq = float(np.mean([b["unique"] for b in byts])) * L
     logical = float(np.mean([b["logical"] for b in byts])) * L
     gbs = uniq / t_step / 1e9
-    gbs_graph = loop.step_bytes()["unique"] * L / t_graph / 1e9
+    gbs_graph = float(np.mean([b["unique"] for b in gbyts])) * L / t_graph / 1e9
     # CPU baseline: the reference's path (gather + fp32 SDPA per sequence, index_put append)
     # for one layer of 4 sequences
     import torch.nn.functional as F
@@ -570,12 +586,15 @@ def step36(args, torch, workloads, dev):
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
         "dtype": "fp16", "data": "synthetic (device-generated N(0,1)*0.5, pages from the manager's pool, NaN-poisoned)",
         "config": {"workload": "qwen2.5-3b 36-layer decode step, B=128, 2048-token shared prefix + own suffix U[64,1024], "
-                               + ("page-table step + plan + append + decode per layer in one graph (device steps)"
-                                  if device_steps else "host page-table step + plan, graph-captured append + decode per layer")
+                               + ("page-table step + plan + decode with the token's append fused in, per layer, "
+                                  "in one graph (device steps)"
+                                  if device_steps else "host page-table step + plan, graph-captured decode with the "
+                                  "token's append fused in, per layer")
                                + ", 8 sequences retired per step",
                    "layers": L, "batch": loop.batch, "steps": steps, "warmup": warmup,
                    "pool_pages": loop.mgr.max_blocks, "device_steps": device_steps},
         "step_ms": round(t_step * 1e3, 4), "graph_ms": round(t_graph * 1e3, 4),
+        "graph_back_to_back_ms": round(t_b2b * 1e3, 4),
         "unique_bytes_per_step": int(uniq), "logical_bytes_per_step": int(logical),
         "graph_unique_gbs": round(gbs_graph, 2), "logical_gbs": round(logical / t_step / 1e9, 2),
         "parity": par,
@@ -782,7 +801,7 @@ def extras(args, torch, runs):
     keep = {
         "qwen25_3b_prefill": ("prefill_us", "prefill_valu_us", "flops"),
         "llama31_8b_b128": ("decode_us", "decode_bytes"),
-        "qwen25_3b_step36": ("step_ms", "graph_ms", "graph_unique_gbs", "parity"),
+        "qwen25_3b_step36": ("step_ms", "graph_ms", "graph_back_to_back_ms", "graph_unique_gbs", "parity"),
         "qwen25_3b_bulk_append": ("by_nnz",),
     }
     out = {}
@@ -931,10 +950,14 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
                 fn()
         return g
 
-    step_graphs = [capture(lambda l=l: (append(l), decode(l))) for l in range(NL)]
+    def decode_append(l):  # the step's append fused into the decode launch
+        w.run(dv.q, kv[l], out=outs[l], append_kv=(dv.k_new, dv.v_new))
+
+    step_graphs = [capture(lambda l=l: decode_append(l)) for l in range(NL)]
     REP = 8  # launches per layer inside the per-kernel timing graphs
     dec_graph = capture(lambda: [decode(l) for _ in range(REP) for l in range(NL)])
     app_graph = capture(lambda: [append(l) for _ in range(REP) for l in range(NL)])
+    fused_graph = capture(lambda: [decode_append(l) for _ in range(REP) for l in range(NL)])
     valu_graph = capture(lambda: [decode_valu(l) for l in range(NL)])
     torch.cuda.synchronize()
 
@@ -963,6 +986,7 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
 
     t_dec = graph_time(torch, stream, dec_graph, n_rep, REP * NL)
     t_app = graph_time(torch, stream, app_graph, n_rep, REP * NL)
+    t_fused = graph_time(torch, stream, fused_graph, n_rep, REP * NL)
     t_valu = graph_time(torch, stream, valu_graph, 1, NL, samples=1)
     torch.cuda.synchronize()
 
@@ -984,7 +1008,8 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
         "data": "synthetic (seeded N(0,1)*0.5 K/V/Q, random page permutation, NaN-poisoned pool)",
         "config": {
             "workload": "qwen2.5-3b paged decode, 1 layer, B=64, ctx U[512,4096], page 16, "
-                        "16 q / 2 kv heads, head_dim 128, fp16, append 1 token/seq then decode",
+                        "16 q / 2 kv heads, head_dim 128, fp16, append 1 token/seq then decode "
+                        "(one launch: the append fused into the decode)",
             "batch": wb.batch,
             "kv_tokens": sum(wb.kv_len),
             "pages": int(wb.indptr[-1]),
@@ -1000,6 +1025,7 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
         "append_mtok_s": round(nnz / t_app / 1e6, 3),
         "append_us": round(t_app * 1e6, 3),
         "append_nnz": nnz,
+        "decode_append_fused_us": round(t_fused * 1e6, 3),
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),
