@@ -212,7 +212,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
 
 
 def prefill_work_list(qo_indptr: list, kv_indptr: list, last_page_len: list, g: int, hkv: int, page_size: int,
-                      causal: bool, head_dim: int, num_cus: int, ws_bytes: int, rows: int = 256) -> dict:
+                      causal: bool, head_dim: int, num_cus: int, ws_bytes: int, rows: int = 256,
+                      partial_bytes: int = 4) -> dict:
     """The matrix-core prefill kernel's work list, on the host.  Items are (request, KV head,
     rows/g query tokens, chunk of the keys those tokens see): the 12 int32 fields
     [b, h, t0, tq, k0, k1, slot, kv_len, qo_len, qo_start, kv_indptr[b], 0].  A key range longer
@@ -220,7 +221,9 @@ def prefill_work_list(qo_indptr: list, kv_indptr: list, last_page_len: list, g: 
     [first slot, chunks, qo_start, t0, tq, h, 0, 0], whose partials a second kernel merges.
     Chunks are whole steps of the kernel (64 keys), sized for about one item per CU: fewer,
     longer items split fewer key ranges (less partial traffic, a shorter merge); they are
-    doubled while the partials would not fit in ``ws_bytes``.  Items are issued longest first."""
+    doubled while the partials would not fit in ``ws_bytes``.  ``partial_bytes`` is the size of
+    one element of a partial output row: 2 for fp16 caches (the kernel keeps their partials in
+    fp16), 4 otherwise.  Items are issued longest first."""
     tq_max = rows // g
     groups = []  # (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b)
     for b in range(len(qo_indptr) - 1):
@@ -250,7 +253,7 @@ def prefill_work_list(qo_indptr: list, kv_indptr: list, last_page_len: list, g: 
         off_g = a(len(items) * 12 * 4)
         off_ml = off_g + a(len(merges) * 8 * 4)
         off_o = off_ml + a(nslots * rows * 8)
-        need = off_o + nslots * rows * head_dim * 4
+        need = off_o + nslots * rows * head_dim * partial_bytes
         if need <= ws_bytes or not merges or chunk >= 8192:
             break
         chunk = min(8192, chunk * 2)
@@ -326,8 +329,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         last = self._last.cpu().tolist()
         self._nnz_q = qo[-1]
         ws_bytes = self._workspace.numel() * self._workspace.element_size()
+        # (the kernel keeps an fp16 cache's split partials in fp16)
         wl = prefill_work_list(qo, kp, last, self._hq // self._hkv, self._hkv, self._ps, self._causal, self._d,
-                               _num_cus(dev), ws_bytes, self._ROWS)
+                               _num_cus(dev), ws_bytes, self._ROWS,
+                               partial_bytes=2 if self._q_dtype == torch.float16 else 4)
         items, merges = wl["items"], wl["groups"]
         off_g, off_ml, off_o = wl["off_groups"], wl["off_ml"], wl["off_o"]
         flat = [x for it in items for x in it] + [0] * ((off_g - len(items) * 48) // 4) + \

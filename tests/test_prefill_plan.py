@@ -76,3 +76,10 @@ def test_chunks_grow_to_fit_the_workspace_or_the_plan_fails():
     assert tight["chunk"] > roomy["chunk"] and tight["bytes"] <= roomy["bytes"] // 2
     with pytest.raises(RuntimeError, match="prefill workspace too small"):
         prefill_work_list(qo, kv, last, 8, 2, 16, True, 128, 256, 4096)
+    # fp16 partials take half the bytes of fp32 ones: a workspace that fp32 partials overflow at
+    # the roomy chunk holds the fp16 plan unchanged
+    fits_half = roomy["off_o"] + (roomy["bytes"] - roomy["off_o"]) // 2
+    assert fits_half < roomy["bytes"]
+    half = prefill_work_list(qo, kv, last, 8, 2, 16, True, 128, 256, fits_half, partial_bytes=2)
+    assert half["chunk"] == roomy["chunk"] and half["slots"] == roomy["slots"]
+    assert half["bytes"] - half["off_o"] == (roomy["bytes"] - roomy["off_o"]) // 2
