@@ -61,7 +61,9 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
          _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
     ),
-    "pkv_pool_apply": (_i32, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _vp, _vp]),
+    "pkv_pool_apply": (_i32, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _vp, _i32, _vp, _vp]),
+    "pkv_pool_copy_pages": (_i32, [_vp, _i64, _i32, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "pkv_shared_prefix_pages": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp]),
     "pkv_pool_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp]),
     "pkv_pool_step": (
         _i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,

@@ -12,8 +12,11 @@
 // launch, in their original order.
 //
 //   pkv_pool_apply   <- allocate / append_tokens / free / init_cuda_graph_buffers, and the
-//                       shared-prefix extension (a sequence's row starts with a copy of the
-//                       prefix's full pages; no counterpart in the reference)
+//                       page-sharing extension (a sequence's row starts with a copy of the
+//                       pages it shares; a shared page written to is replaced by a private
+//                       copy; no counterpart in the reference)
+//   pkv_pool_copy_pages, pkv_shared_prefix_pages <- the same extension: the K/V data of those
+//                       copies, and the decode plan's shared-page hint from the page lists
 //   pkv_pool_gather  <- get_append_metadata / fill_cuda_graph_metadata (the page walk that
 //                       builds kv_indices, manager.py:124-133, 231-246)
 //   pkv_pool_step    <- one decode step of a fixed batch, all on the device: append_tokens(b, n)
@@ -32,21 +35,33 @@ namespace {
 // push of the same batch wrote).  Operation i is ops[5i .. 5i+4] = {kind, row, pos, col, n}:
 //   kind 0, pop:  table[row][col + k] = stack[pos - 1 - k]   (k < n: the order of pop())
 //   kind 1, push: stack[pos + k] = table[row][col + k]       (the order of extend())
-//   kind 2, copy: table[row][col + k] = table[pos][k]         (pos = the prefix's row)
-// Operations that fall outside the stack or the table are skipped and counted in *err.
+//   kind 2, copy: table[row][col + k] = table[pos][k]         (pos = the sharer's source row)
+//   kind 3, copy on write: the page table[row][col] is replaced by stack[pos - 1] (one pop),
+//           and pairs[2n], pairs[2n + 1] = (old page, new page) for the data copy
+// Operations that fall outside the stack, the table or the pairs are skipped and counted in
+// *err.
 __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
-                                  int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err) {
+                                  int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* pairs,
+                                  int32_t pairs_cap, int32_t* err) {
   __shared__ int32_t s_op[5];
   for (int i = 0; i < n_ops; ++i) {
     if (threadIdx.x < 5) s_op[threadIdx.x] = ops[5 * i + threadIdx.x];
     __syncthreads();
     const int kind = s_op[0], row = s_op[1], pos = s_op[2], col = s_op[3], n = s_op[4];
-    bool ok = kind >= 0 && kind <= 2 && row >= 0 && row < rows && col >= 0 && n >= 0 && (int64_t)col + n <= stride;
-    if (kind == 0) ok = ok && pos - n >= 0 && pos <= stack_size;
-    else if (kind == 1) ok = ok && pos >= 0 && pos + n <= stack_size;
-    else ok = ok && pos >= 0 && pos < rows && pos != row && n <= stride;
+    bool ok = kind >= 0 && kind <= 3 && row >= 0 && row < rows && col >= 0 && n >= 0;
+    if (kind == 0) ok = ok && (int64_t)col + n <= stride && pos - n >= 0 && pos <= stack_size;
+    else if (kind == 1) ok = ok && (int64_t)col + n <= stride && pos >= 0 && pos + n <= stack_size;
+    else if (kind == 2) ok = ok && (int64_t)col + n <= stride && pos >= 0 && pos < rows && pos != row;
+    else ok = ok && col < stride && pos >= 1 && pos <= stack_size && pairs && n < pairs_cap;
     if (!ok) {
       if (threadIdx.x == 0 && err) atomicAdd(err, 1);
+    } else if (kind == 3) {
+      if (threadIdx.x == 0) {
+        int32_t* cell = table + (int64_t)row * stride + col;
+        pairs[2 * n] = *cell;
+        pairs[2 * n + 1] = stack[pos - 1];
+        *cell = stack[pos - 1];
+      }
     } else {
       int32_t* trow = table + (int64_t)row * stride + col;
       const int32_t* src = table + (int64_t)pos * stride;  // (kind 2 only)
@@ -58,6 +73,49 @@ __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* t
     }
     __syncthreads();  // this operation's writes are visible to the next one
   }
+}
+
+// The data of copy-on-write pairs: for pair p and layer l (blockIdx.y, blockIdx.z), the page
+// pairs[2p] of the layer is copied to the page pairs[2p + 1], 16 bytes per thread (the page is
+// whole 16-byte runs: 2 x page_size x Hkv x head_dim elements).  Pairs naming a page outside
+// the pool are skipped and counted in *err.
+__global__ void pool_copy_pages_kernel(char* cache, int64_t layer_stride, int64_t page_bytes, const int32_t* pairs,
+                                       int64_t num_pages, int32_t* err) {
+  const int p = blockIdx.y, l = blockIdx.z;
+  const int src = pairs[2 * p], dst = pairs[2 * p + 1];
+  if (src < 0 || src >= num_pages || dst < 0 || dst >= num_pages) {
+    if (err && l == 0 && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(err, 1);
+    return;
+  }
+  const char* from = cache + l * layer_stride + (int64_t)src * page_bytes;
+  char* to = cache + l * layer_stride + (int64_t)dst * page_bytes;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < page_bytes / 16;
+       c += (int64_t)gridDim.x * blockDim.x)
+    reinterpret_cast<uint4*>(to)[c] = reinterpret_cast<const uint4*>(from)[c];
+}
+
+// out[b] = how many leading page ids rows b and b - 1 of the page table have in common (the
+// decode plan's kv_shared_pages hint), out[0] = 0; one wave per row, 64 ids compared at a time.
+__global__ void shared_prefix_kernel(const int32_t* __restrict__ indptr, const int32_t* __restrict__ indices,
+                                     int64_t num_indices, int32_t batch, int32_t* __restrict__ out) {
+  const int b = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6), lane = threadIdx.x & 63;
+  if (b >= batch) return;
+  int k = 0;
+  if (b > 0) {
+    const int64_t x0 = indptr[b], x1 = indptr[b + 1], y0 = indptr[b - 1];
+    int64_t n = x1 - x0 < x0 - y0 ? x1 - x0 : x0 - y0;
+    if (x1 > num_indices || x0 < 0 || y0 < 0) n = 0;
+    for (int64_t i = 0; i < n; i += 64) {
+      const bool diff = i + lane < n && indices[x0 + i + lane] != indices[y0 + i + lane];
+      const uint64_t bal = __ballot(diff);
+      if (bal) {
+        k = (int)(i + __builtin_ctzll(bal));
+        break;
+      }
+      k = (int)(i + 64 < n ? i + 64 : n);
+    }
+  }
+  if (lane == 0) out[b] = k;
 }
 
 // indices[indptr[b] + k] = table[desc[4b]][desc[4b+1] + k] for k < desc[4b+2]; one thread per
@@ -205,12 +263,37 @@ __global__ __launch_bounds__(kStepThreads) void pool_step_kernel(
 }  // namespace
 
 extern "C" int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
-                              int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err,
-                              void* stream) {
-  if (n_ops < 0 || stack_size < 0 || stride <= 0 || rows <= 0) return kBadArg;
+                              int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* pairs,
+                              int32_t pairs_cap, int32_t* err, void* stream) {
+  if (n_ops < 0 || stack_size < 0 || stride <= 0 || rows <= 0 || pairs_cap < 0) return kBadArg;
   if (n_ops == 0) return kOk;
   hipLaunchKernelGGL(pool_apply_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, stack, stack_size,
-                     table, stride, rows, ops, n_ops, err);
+                     table, stride, rows, ops, n_ops, pairs, pairs_cap, err);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_pool_copy_pages(void* cache, int64_t layer_stride, int32_t layers, int64_t page_bytes,
+                                   const int32_t* pairs, int32_t n_pairs, int64_t num_pages, int32_t* err,
+                                   void* stream) {
+  if (layers < 0 || n_pairs < 0 || page_bytes <= 0 || page_bytes % 16 || layer_stride % 16 || num_pages < 0 ||
+      (uintptr_t)cache % 16)
+    return kBadArg;
+  if (layers == 0 || n_pairs == 0) return kOk;
+  if (n_pairs > 65535 || layers > 65535) return kBadArg;
+  const int64_t chunks = page_bytes / 16;
+  const unsigned bx = (unsigned)((chunks + 255) / 256 < 64 ? (chunks + 255) / 256 : 64);
+  hipLaunchKernelGGL(pool_copy_pages_kernel, dim3(bx, (unsigned)n_pairs, (unsigned)layers), dim3(256), 0,
+                     (hipStream_t)stream, (char*)cache, layer_stride, page_bytes, pairs, num_pages, err);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_shared_prefix_pages(const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
+                                       int32_t batch, int32_t* out, void* stream) {
+  if (batch < 0 || num_indices < 0) return kBadArg;
+  if (batch == 0) return kOk;
+  const unsigned blocks = (unsigned)((batch + 3) / 4);  // 4 waves per block, one per row
+  hipLaunchKernelGGL(shared_prefix_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, kv_indptr, kv_indices,
+                     num_indices, batch, out);
   return (int)hipGetLastError();
 }
 

@@ -28,10 +28,16 @@ with ``T % block_size == 0`` records ``block_size`` as the last page's length in
 ``T`` tokens are held; ``strict_reference_q1=True`` restores it.
 
 One extension with no counterpart in the reference (which has no page refcounting, so its
-sequences cannot share pages): ``allocate(b, T, prefix=p)`` starts sequence b's page list
-with the full pages of the live sequence p (copied on the device, not popped) and pops pages
-for the rest of its T tokens; ``free(b)`` pushes back only b's own pages, and ``free(p)``
-raises while any sequence shares p.  The oracle restates the same rules.
+sequences cannot share pages): radix-style page sharing.  ``allocate(b, T, prefix=p)`` starts
+sequence b's page list with the pages of the live sequence p that cover its first min(T,
+len(p)) tokens (copied on the device, not popped; p's partial last page included, and p may
+itself share pages, so prefixes nest) and pops pages for the rest.  Every page has a count of
+the lists that hold it (on the host, under a handle given out at each pop): a sequence whose
+tokens would go into a page others hold first takes a private copy of it (one pop; the page's
+K/V copied on the device for every layer), at allocate or at append_tokens; ``free(b)``
+returns, in page order, the pages only b held (a tail of its list) and drops the counts of
+the rest.  The oracle restates the same rules; the graph metadata's shared-page hint for the
+decode plan is computed on the device from the page lists.
 
 The sampling helpers (init_sampling_buffers, fill_sampling_params,
 fill_cuda_graph_sampling_params, ``mask_penalty``) are outside the paged-KV path; they are
@@ -49,7 +55,7 @@ from ._lib import check, lib, stream_ptr
 from .ops import (append_paged_kv_cache, append_paged_kv_cache_slots, get_batch_indices_positions,
                   get_seq_lens)
 
-_POP, _PUSH, _COPY = 0, 1, 2
+_POP, _PUSH, _COPY, _COW = 0, 1, 2, 3
 
 
 def get_total_free_memory(index: int = 0) -> int:
@@ -220,8 +226,15 @@ class AutoKVCacheManager:
         self._staging = _Staging(self.device)
         self._ops: list = []
         self._n_padding = 0
-        self._shared: dict = {}  # batch_id -> (prefix id, leading shared pages)
-        self._refs: dict = {}    # prefix id -> live sequences sharing its pages
+        # page sharing (an extension): each page in a list has a host-side handle (one per pop)
+        # and a count of the lists that hold it; the page ids themselves stay on the device
+        self._pg: dict = {}      # batch_id -> handles of its pages, in page order
+        self._rc: dict = {}      # handle -> lists holding that page
+        self._next_handle = 0
+        self._n_multi = 0        # handles held by more than one list
+        self._n_cow = 0          # copies on write queued since the last flush
+        self._cow_cap = 1024
+        self._pairs = torch.zeros(2 * self._cow_cap, dtype=torch.int32, device=self.device)
 
         # host bookkeeping: counts only
         self.free_seq_lens = list(range(self.seq_lens))
@@ -263,7 +276,8 @@ class AutoKVCacheManager:
         self._table, self._stride = table, new
 
     def _flush(self) -> None:
-        """Apply the queued pops and pushes (one launch, in order, on the current stream)."""
+        """Apply the queued pops, pushes and copies (one launch, in order, on the current
+        stream), then copy the K/V data of the queued copies on write."""
         self._end_dev()
         if not self._ops:
             return
@@ -271,8 +285,55 @@ class AutoKVCacheManager:
         ops = self._staging.copy(flat)
         check(lib().pkv_pool_apply(self._stack.data_ptr(), self.max_blocks, self._table.data_ptr(),
                                    self._stride, self._rows, ops.data_ptr(), len(self._ops),
-                                   self._err.data_ptr(), stream_ptr(self.device)), "page pool update")
+                                   self._pairs.data_ptr(), self._cow_cap, self._err.data_ptr(),
+                                   stream_ptr(self.device)), "page pool update")
         self._ops = []
+        if self._n_cow:
+            c = self.kv_cache
+            check(lib().pkv_pool_copy_pages(c.data_ptr(), c.stride(0) * c.element_size(), c.shape[0],
+                                            c.stride(1) * c.element_size(), self._pairs.data_ptr(), self._n_cow,
+                                            self.max_blocks, self._err.data_ptr(), stream_ptr(self.device)),
+                  "page copy")
+            self._n_cow = 0
+
+    # ------------------------------------------------------------------ page handles (sharing)
+
+    def _new_handles(self, n: int) -> list:
+        h = list(range(self._next_handle, self._next_handle + n))
+        self._next_handle += n
+        for x in h:
+            self._rc[x] = 1
+        return h
+
+    def _hold(self, handles) -> None:
+        for x in handles:
+            self._rc[x] += 1
+            if self._rc[x] == 2:
+                self._n_multi += 1
+
+    def _drop(self, x) -> None:
+        self._rc[x] -= 1
+        if self._rc[x] == 1:
+            self._n_multi -= 1
+        elif self._rc[x] == 0:
+            del self._rc[x]
+
+    def _shares_last_page(self, batch_id) -> bool:
+        """Whether new tokens of batch_id would go into a page other lists hold."""
+        h = self._pg.get(batch_id)
+        return bool(h) and self._rc[h[-1]] > 1 and self.batch_to_page_lengths[batch_id] < self.block_size
+
+    def _queue_cow(self, batch_id) -> None:
+        """Replace batch_id's (shared) last page by a private copy: one pop from the top of the
+        stack; the page's K/V is copied for every layer when the queue is applied."""
+        if self._n_cow == self._cow_cap:
+            self._flush()
+        h = self._pg[batch_id]
+        self._ops.append((_COW, self.batch_to_seq_len[batch_id], self._n_free, len(h) - 1, self._n_cow))
+        self._n_cow += 1
+        self._n_free -= 1
+        self._drop(h[-1])
+        h[-1] = self._new_handles(1)[0]
 
     def _stage_tables(self, ids: list, bucket: int = 0, positions: bool = False) -> tuple:
         """The gather's input for the sequences ``ids`` followed by ``bucket - len(ids)``
@@ -309,13 +370,7 @@ class AutoKVCacheManager:
             pos[:r] += plen - 1
             pos[r:] = 0
             shared = out[7 * b + 1: 8 * b + 1]
-            shared[:] = 0
-            if self._shared and r > 1:
-                sh = [self._shared.get(i) for i in ids]
-                for k in range(1, r):
-                    a, c = sh[k - 1], sh[k]
-                    if a is not None and c is not None and a[0] == c[0]:
-                        shared[k] = min(a[1], c[1])
+            shared[:] = 0  # (filled on the device from the gathered lists when pages are shared)
         return slot, out, b, int(indptr[-1])
 
     def _gather(self, slot: int, staged: np.ndarray, b: int, pages: int, out_indices: torch.Tensor,
@@ -390,63 +445,74 @@ class AutoKVCacheManager:
 
     def allocate(self, batch_id, total_tokens: int, *, prefix=None) -> _Pages:
         """manager.py:99-112: pop ceil(T / block_size) pages, take a sequence slot.  With
-        ``prefix`` (an extension), the full pages of that live sequence come first and only
-        the rest are popped."""
+        ``prefix`` (an extension), the pages of that live sequence covering the first
+        min(T, len(prefix)) tokens come first (a partial last page included; copied, if this
+        sequence's tokens continue into it) and only the rest are popped."""
         self._end_dev()
-        shared = 0
+        bs = self.block_size
+        k, cow = 0, False
         if prefix is not None:
             if prefix not in self._npages:
                 raise ValueError(f"{prefix} not allocated")
-            shared = self._seq_len(prefix) // self.block_size
-            if total_tokens < shared * self.block_size:
-                raise ValueError("a sequence cannot be shorter than its shared prefix")
-        num_pages = math.ceil(total_tokens / self.block_size) - shared
-        if self._n_free < num_pages:
+            ts = min(total_tokens, self._seq_len(prefix))
+            k = math.ceil(ts / bs)
+            cow = total_tokens > ts and ts % bs != 0
+        num_pages = math.ceil(total_tokens / bs) - k
+        if self._n_free < num_pages + cow:
             raise RuntimeError("Not enough KV cache blocks available")
         if not self.free_seq_lens:
             raise IndexError("pop from empty list")
         slot = self.free_seq_lens.pop()
-        self._ensure_stride(shared + num_pages)
-        if prefix is not None:  # (a prefix with no full page yet is still held)
-            self._shared[batch_id] = (prefix, shared)
-            self._refs[prefix] = self._refs.get(prefix, 0) + 1
-        if shared:
-            self._ops.append((_COPY, slot, self.batch_to_seq_len[prefix], 0, shared))
+        self._ensure_stride(k + num_pages)
+        handles = []
+        if k:
+            handles = self._pg[prefix][:k]
+            self._hold(handles)
+            self._ops.append((_COPY, slot, self.batch_to_seq_len[prefix], 0, k))
+        self._pg[batch_id] = handles
+        self.batch_to_seq_len[batch_id] = slot
+        if cow:
+            self.batch_to_page_lengths[batch_id] = 0  # (read by nothing before it is set below)
+            self._queue_cow(batch_id)
         if num_pages:
-            self._ops.append((_POP, slot, self._n_free, shared, num_pages))
+            self._ops.append((_POP, slot, self._n_free, k, num_pages))
             self._n_free -= num_pages
-        num_pages += shared
-        self._npages[batch_id] = num_pages
-        page_len = total_tokens % self.block_size
+            handles += self._new_handles(num_pages)
+        self._npages[batch_id] = k + num_pages
+        page_len = total_tokens % bs
         if page_len == 0 and total_tokens > 0 and not self.strict_reference_q1:
-            page_len = self.block_size
+            page_len = bs
         self.batch_to_page_lengths[batch_id] = page_len
         self.batch_to_total_tokens[batch_id] = total_tokens
-        self.batch_to_seq_len[batch_id] = slot
         self.mask_penalty[slot] = 1.0
-        return _Pages(self, slot, num_pages)
+        return _Pages(self, slot, k + num_pages)
 
     def free(self, batch_id) -> None:
-        """manager.py:114-120: push the pages back in page order, release the slot (a
-        sequence's shared prefix pages stay with the prefix)."""
+        """manager.py:114-120: push the pages back in page order, release the slot.  With
+        shared pages (an extension), only the pages no other list holds go back: always a tail
+        of the list, since a list holding one of this sequence's pages holds all before it."""
         self._end_dev()
-        if self._refs.get(batch_id):
-            raise RuntimeError(f"{batch_id} is the shared prefix of {self._refs[batch_id]} live sequences")
+        handles = self._pg.pop(batch_id, [])
         n = self._npages.pop(batch_id, 0)
         self.batch_to_page_lengths.pop(batch_id, None)
         slot = self.batch_to_seq_len.pop(batch_id, None)
-        prefix, shared = self._shared.pop(batch_id, (None, 0))
-        if prefix is not None:
-            self._refs[prefix] -= 1
-        if n > shared and slot is not None:
-            self._ops.append((_PUSH, slot, self._n_free, shared, n - shared))
-            self._n_free += n - shared
+        t = len(handles)
+        while t > 0 and self._rc[handles[t - 1]] == 1:
+            t -= 1
+        if any(self._rc[x] == 1 for x in handles[:t]):
+            raise RuntimeError("page sharing bookkeeping is inconsistent")
+        for x in handles:
+            self._drop(x)
+        if n > t and slot is not None:
+            self._ops.append((_PUSH, slot, self._n_free, t, n - t))
+            self._n_free += n - t
         if slot is not None:
             self.free_seq_lens.append(slot)
 
     def append_tokens(self, batch_id, num_new_tokens: int) -> None:
         """manager.py:187-205: a page is popped as soon as the last one fills (an empty
-        trailing page with last_page_len 0 is kept, as the reference does)."""
+        trailing page with last_page_len 0 is kept, as the reference does).  New tokens that
+        would go into a page other sequences hold (an extension) first get a private copy of it."""
         self._end_dev()
         if batch_id not in self._npages:
             raise ValueError(f"{batch_id} not allocated")
@@ -454,14 +520,18 @@ class AutoKVCacheManager:
         total_tokens = current_len + num_new_tokens
         full_new_pages = total_tokens // self.block_size
         remaining = total_tokens % self.block_size
-        if full_new_pages > self._n_free:
+        cow = num_new_tokens > 0 and self._shares_last_page(batch_id)
+        if full_new_pages + cow > self._n_free:
             raise RuntimeError("Not enough free blocks to append tokens")
+        if cow:
+            self._queue_cow(batch_id)
         if full_new_pages:
             col = self._npages[batch_id]
             self._ensure_stride(col + full_new_pages)
             self._ops.append((_POP, self.batch_to_seq_len[batch_id], self._n_free, col, full_new_pages))
             self._n_free -= full_new_pages
             self._npages[batch_id] = col + full_new_pages
+            self._pg[batch_id] += self._new_handles(full_new_pages)
         self.batch_to_page_lengths[batch_id] = remaining
 
     # ------------------------------------------------------------------ page tables (A6-A9)
@@ -550,8 +620,9 @@ class AutoKVCacheManager:
         """manager.py:228-253: the real sequences' page tables and the position of each one's
         newest token, then ``bucket - n`` padding rows (one padding page, last_page_len 1,
         position 0), written into the bucket's static buffers on the device.  Also fills
-        ``_cg_kv_shared[bucket]``: for consecutive rows allocated on the same prefix, the
-        prefix pages they share (the decode plan's ``kv_shared_pages``)."""
+        ``_cg_kv_shared[bucket]``: for each row, the leading pages it has in common with the
+        row before it (the decode plan's ``kv_shared_pages``; all zero unless pages are
+        shared)."""
         real_uuids = list(real_uuids)
         self._flush()
         slot, staged, b, pages = self._stage_tables(real_uuids, bucket_size, positions=True)
@@ -561,6 +632,11 @@ class AutoKVCacheManager:
         # the step reads are views of it
         self._gather(slot, staged, b, pages, self._cg_kv_indices[bucket_size], dst=self._cg_meta[bucket_size],
                      slots=self._cg_slots[bucket_size])
+        if self._n_multi:
+            idx = self._cg_kv_indices[bucket_size]
+            check(lib().pkv_shared_prefix_pages(self._cg_kv_indptr[bucket_size].data_ptr(), idx.data_ptr(),
+                                                idx.numel(), b, self._cg_kv_shared[bucket_size].data_ptr(),
+                                                stream_ptr(self.device)), "shared-page hint")
 
     def append_paged_kv_cache_cuda_graph(self, key, value, bucket_size: int, layer_idx: int) -> None:
         """manager.py:270-280: the append through the bucket's static metadata.  Each row's
@@ -590,6 +666,23 @@ class AutoKVCacheManager:
         bs = self.block_size
         if steps < 0 or num_new_tokens < 0:
             raise ValueError("steps and num_new_tokens must be non-negative")
+        if steps and num_new_tokens:
+            # A row whose new tokens would go into a page other lists hold takes its private
+            # copy now (the copy on write its first append would make), in row order, so the
+            # device steps only ever write pages their rows hold alone.
+            rc, need = {}, 0
+            for i in ids:  # (a copy drops the old page's count for the rows after it)
+                h = self._pg[i]
+                if h and self.batch_to_page_lengths[i] < bs:
+                    c = rc.get(h[-1], self._rc[h[-1]])
+                    if c > 1:
+                        rc[h[-1]] = c - 1
+                        need += 1
+            if need > self._n_free:
+                raise RuntimeError("Not enough free blocks to append tokens")
+            for i in ids:
+                if self._shares_last_page(i):
+                    self._queue_cow(i)
         grow = -(-(steps * num_new_tokens) // bs) + 1  # pages a sequence can gain
         if ids:
             self._ensure_stride(max(self._npages[i] for i in ids) + grow)
@@ -671,6 +764,8 @@ class AutoKVCacheManager:
         self._dev = None
         for i, n0, p0 in zip(d["ids"], d["npages0"], d["plen0"]):
             self._npages[i], self.batch_to_page_lengths[i] = self._advanced(n0, p0, d["k"] * d["n"])
+            if self._npages[i] > n0:  # the pages the device steps popped
+                self._pg[i] += self._new_handles(self._npages[i] - n0)
 
     # ------------------------------------------------------------------ sampling buffers (outside the path)
     # main.py reads sampling_{temperature,top_k,top_p}_gpu and the bucket's _cg_* copies of

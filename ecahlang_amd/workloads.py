@@ -317,7 +317,7 @@ class SharedPrefixDecodeLoop:
         tokens = self.prefix_tokens + n
         self.mgr.allocate(sid, tokens, prefix="prefix")
         self._note(("allocate", sid, tokens, "prefix"))
-        self._write_tokens(sid, self.mgr._shared[sid][1])
+        self._write_tokens(sid, self.prefix_tokens // self.ps)  # (its pages after the prefix's full ones)
         return sid
 
     # ---------------------------------------------------------------- one step

@@ -265,11 +265,30 @@ int pkv_batch_prefill_mfma(const void* q, int64_t q_stride_n, int64_t q_stride_h
  *     table[row][col + k] = stack[pos - 1 - k] for k < n
  *   kind 1, push (free :116): stack[pos + k] = table[row][col + k] for k < n
  *   kind 2, copy: table[row][col + k] = table[pos][k] for k < n (a sequence that shares the
- *     full pages of a prefix sequence in row pos; the reference has no prefix sharing, so this
- *     kind has no counterpart there)
- * Operations outside the stack or table are skipped and counted in *err (may be NULL). */
+ *     leading pages of the sequence in row pos; the reference has no page sharing, so this
+ *     kind and the next have no counterpart there)
+ *   kind 3, copy on write: table[row][col] = stack[pos - 1] (one pop), after writing the old
+ *     and the new page id to pairs[2n], pairs[2n + 1] (n < pairs_cap) for
+ *     pkv_pool_copy_pages
+ * Operations outside the stack, table or pairs are skipped and counted in *err (may be NULL). */
 int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
-                   int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* err, void* stream);
+                   int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* pairs, int32_t pairs_cap,
+                   int32_t* err, void* stream);
+
+/* The K/V data of n_pairs copy-on-write pairs (the page-sharing extension of AutoKVCacheManager;
+ * no counterpart in the reference): for every layer l < layers, the page_bytes bytes of page
+ * pairs[2p] at cache + l * layer_stride are copied to page pairs[2p + 1] (byte offsets
+ * page * page_bytes).  16-byte aligned; pairs naming pages outside [0, num_pages) are skipped
+ * and counted in *err (may be NULL). */
+int pkv_pool_copy_pages(void* cache, int64_t layer_stride, int32_t layers, int64_t page_bytes,
+                        const int32_t* pairs, int32_t n_pairs, int64_t num_pages, int32_t* err,
+                        void* stream);
+
+/* The decode plan's kv_shared_pages from a page table (the page-sharing extension; no
+ * counterpart in the reference): out[b] = the number of leading page ids rows b and b - 1
+ * have in common, out[0] = 0.  Rows past num_indices count as sharing nothing. */
+int pkv_shared_prefix_pages(const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
+                            int32_t batch, int32_t* out, void* stream);
 
 /* The page walk of get_append_metadata / fill_cuda_graph_metadata (ecahlang/manager.py:124-133,
  * :231-246): kv_indices[indptr[b] + k] = table[desc[4b]][desc[4b+1] + k] for k < desc[4b+2],

@@ -9,11 +9,19 @@ One deliberate divergence, shared with the product manager: ``allocate(T)`` with
 (and a following append overwrites slot 0 of the last full page); block_size is the only
 value consistent with the pages it pops.  The page ids popped are unchanged.
 
-One extension with no counterpart in the reference (which has no page refcounting): prefix
-sharing.  ``allocate(b, T, prefix=p)`` gives sequence b the full pages of the live sequence p
-first (shared, not popped), then pops the pages for the rest of its T tokens; ``free(b)``
-returns only b's own pages; ``free(p)`` while sequences share p raises.  This is the
-restatement the device manager's prefix sharing is checked against.
+One extension with no counterpart in the reference (which has no page refcounting): shared
+pages, radix style.  Every page in a sequence's list has a reference count (the number of
+lists that hold it).  ``allocate(b, T, prefix=p)`` gives sequence b the pages of the live
+sequence p that cover b's first min(T, len(p)) tokens -- p's partial last page included --
+then pops pages for the rest of its T tokens; p may itself share pages with others, so
+prefixes nest.  A sequence that writes into a page others still hold first takes a private
+copy of it ("copy on write": one page popped, the old page's count dropped; the device copies
+the page's K/V for every layer): at allocate, when b's tokens continue past a shared partial
+page, and at append_tokens, when new tokens go into a shared last page.  Those pops come
+before the others of the same call.  ``free(b)`` returns, in page order, the pages only b
+held (always a tail of b's list: every sequence that holds one of b's pages holds all of b's
+pages before it) and drops the counts of the rest.  This is the restatement the device
+manager's sharing is checked against.
 """
 from __future__ import annotations
 
@@ -35,26 +43,45 @@ class RefKVCacheManager:
         self.batch_to_seq_len: dict = {}
         self.padding_pages: list = []
         self.strict_reference_q1 = strict_reference_q1
-        self.shared: dict = {}  # batch_id -> (prefix id, number of leading shared pages)
-        self.refs: dict = {}    # prefix id -> live sequences sharing its pages
+        self.refs: dict = {}    # page id -> number of sequences whose list holds it
+        self.cow_pairs: list = []  # (old page, new page) of every copy on write, in order
 
-    # manager.py:99-112 (+ the prefix extension)
+    def _pop(self) -> int:
+        page = self.free_blocks.pop()
+        self.refs[page] = 1
+        return page
+
+    def _cow(self, blocks: list, i: int) -> None:
+        """Replace the shared page blocks[i] by a private copy."""
+        old, new = blocks[i], self._pop()
+        self.refs[old] -= 1
+        blocks[i] = new
+        self.cow_pairs.append((old, new))
+
+    def shares_last_page(self, batch_id) -> bool:
+        """Whether new tokens would go into a page other sequences hold."""
+        pages = self.batch_to_blocks[batch_id]
+        return bool(pages) and self.refs[pages[-1]] > 1 and self.batch_to_page_lengths[batch_id] < self.block_size
+
+    # manager.py:99-112 (+ the sharing extension)
     def allocate(self, batch_id, total_tokens: int, prefix=None) -> list:
-        shared = []
+        shared, cow = [], False
         if prefix is not None:
             if prefix not in self.batch_to_blocks:
                 raise ValueError(f"{prefix} not allocated")
-            shared = self.batch_to_blocks[prefix][: self.seq_len(prefix) // self.block_size]
-            if total_tokens < len(shared) * self.block_size:
-                raise ValueError("a sequence cannot be shorter than its shared prefix")
+            ts = min(total_tokens, self.seq_len(prefix))
+            shared = self.batch_to_blocks[prefix][: math.ceil(ts / self.block_size)]
+            cow = total_tokens > ts and ts % self.block_size != 0
         num_pages = math.ceil(total_tokens / self.block_size) - len(shared)
-        if len(self.free_blocks) < num_pages:
+        if len(self.free_blocks) < num_pages + cow:
             raise RuntimeError("Not enough KV cache blocks available")
-        blocks = shared + [self.free_blocks.pop() for _ in range(num_pages)]
+        blocks = list(shared)
+        for page in shared:
+            self.refs[page] += 1
+        if cow:
+            self._cow(blocks, len(blocks) - 1)
+        blocks += [self._pop() for _ in range(num_pages)]
         self.batch_to_blocks[batch_id] = blocks
-        if prefix is not None:
-            self.shared[batch_id] = (prefix, len(shared))
-            self.refs[prefix] = self.refs.get(prefix, 0) + 1
         page_len = total_tokens % self.block_size
         if page_len == 0 and total_tokens > 0 and not self.strict_reference_q1:
             page_len = self.block_size
@@ -64,21 +91,24 @@ class RefKVCacheManager:
         self.batch_to_seq_len[batch_id] = seq_slot
         return blocks
 
-    # manager.py:114-120 (+ the prefix extension)
+    # manager.py:114-120 (+ the sharing extension)
     def free(self, batch_id) -> None:
-        if self.refs.get(batch_id):
-            raise RuntimeError(f"{batch_id} is the shared prefix of {self.refs[batch_id]} live sequences")
         blocks = self.batch_to_blocks.pop(batch_id, [])
-        prefix, n_shared = self.shared.pop(batch_id, (None, 0))
-        if prefix is not None:
-            self.refs[prefix] -= 1
-        self.free_blocks.extend(blocks[n_shared:])
+        t = len(blocks)
+        while t > 0 and self.refs[blocks[t - 1]] == 1:
+            t -= 1
+        assert all(self.refs[p] > 1 for p in blocks[:t]), "pages only this list holds form its tail"
+        for p in blocks[:t]:
+            self.refs[p] -= 1
+        for p in blocks[t:]:
+            del self.refs[p]
+        self.free_blocks.extend(blocks[t:])
         self.batch_to_page_lengths.pop(batch_id, None)
         seq_slot = self.batch_to_seq_len.pop(batch_id, None)
         if seq_slot is not None:
             self.free_seq_lens.append(seq_slot)
 
-    # manager.py:187-205
+    # manager.py:187-205 (+ copy on write into a shared last page)
     def append_tokens(self, batch_id, num_new_tokens: int) -> None:
         if batch_id not in self.batch_to_blocks:
             raise ValueError(f"{batch_id} not allocated")
@@ -86,11 +116,43 @@ class RefKVCacheManager:
         total_tokens = current_len + num_new_tokens
         full_new_pages = total_tokens // self.block_size
         remaining = total_tokens % self.block_size
-        if full_new_pages > len(self.free_blocks):
+        cow = num_new_tokens > 0 and self.shares_last_page(batch_id)
+        if full_new_pages + cow > len(self.free_blocks):
             raise RuntimeError("Not enough free blocks to append tokens")
+        if cow:
+            self._cow(self.batch_to_blocks[batch_id], len(self.batch_to_blocks[batch_id]) - 1)
         for _ in range(full_new_pages):
-            self.batch_to_blocks[batch_id].append(self.free_blocks.pop())
+            self.batch_to_blocks[batch_id].append(self._pop())
         self.batch_to_page_lengths[batch_id] = remaining
+
+    def make_last_pages_private(self, batch_ids) -> None:
+        """Copy on write, in list order, for every sequence whose new tokens would go into a
+        shared page (what each one's next append_tokens would do first)."""
+        refs, need = dict(self.refs), 0
+        for b in batch_ids:  # (a copy drops the old page's count for the rows after it)
+            pages = self.batch_to_blocks[b]
+            if pages and refs[pages[-1]] > 1 and self.batch_to_page_lengths[b] < self.block_size:
+                refs[pages[-1]] -= 1
+                need += 1
+        if need > len(self.free_blocks):
+            raise RuntimeError("Not enough free blocks to append tokens")
+        for b in batch_ids:
+            if self.shares_last_page(b):
+                self._cow(self.batch_to_blocks[b], len(self.batch_to_blocks[b]) - 1)
+
+    @staticmethod
+    def shared_prefix_pages(kv_indices: list, kv_indptr: list) -> list:
+        """Entry b >= 1: how many leading pages row b has in common with row b - 1 (the
+        decode plan's kv_shared_pages); entry 0 is 0."""
+        out = [0] * (len(kv_indptr) - 1)
+        for b in range(1, len(out)):
+            x = kv_indices[kv_indptr[b]:kv_indptr[b + 1]]
+            y = kv_indices[kv_indptr[b - 1]:kv_indptr[b]]
+            k = 0
+            while k < min(len(x), len(y)) and x[k] == y[k]:
+                k += 1
+            out[b] = k
+        return out
 
     # manager.py:122-138 (lists instead of device tensors)
     def get_append_metadata(self, batch_ids) -> tuple:

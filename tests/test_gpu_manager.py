@@ -217,29 +217,39 @@ def test_end_to_end_prefill_then_decode_steps():
     assert m.pool_errors() == 0
 
 
-@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("seed", [0, 1, 2])
 def test_prefix_sharing_matches_oracle(seed):
-    """The prefix extension (allocate(..., prefix=)) against the oracle's restatement: page
-    lists, free stack and exceptions, under random allocate / share / append / free."""
+    """Page sharing (allocate(..., prefix=), nested, shorter and longer than the prefix, with
+    copies on write at allocate and at append) against the oracle's restatement: page lists,
+    free stack and exceptions under random allocate / share / append / free; the graph
+    metadata's shared-page hint against the lists the oracle holds."""
     rng = random.Random(100 + seed)
     P = 120
-    dev, ref = _pool(P), RefKVCacheManager(P)
-    ids = list(range(10))
-    for step in range(300):
-        kind = rng.choice(["alloc", "share", "share", "append", "append", "free", "meta"])
+    dev, ref = _pool(P, stride=16), RefKVCacheManager(P)
+    dev.init_cuda_graph_buffers([16], max_indices=4096)
+    ref.init_cuda_graph_buffers([16])
+    ids = list(range(12))
+    for step in range(400):
+        kind = rng.choice(["alloc", "share", "share", "share", "append", "append", "free", "meta", "hint"])
         sid = rng.choice(ids)
         n = rng.choice([0, 1, 2, 15, 16, 17, 33, 70])
+        live = sorted(s for s in ids if s in ref.batch_to_blocks)
         if kind == "meta":
-            live = [s for s in ids if s in ref.batch_to_blocks]
             idx, ptr, last = dev.get_append_metadata(live)
             assert (idx.tolist(), ptr.tolist(), last.tolist()) == tuple(map(list, ref.get_append_metadata(live)))
             continue
+        if kind == "hint":
+            rows = rng.sample(live, min(len(live), 16))
+            rows.sort(key=lambda i: ref.batch_to_blocks[i][:1])  # sharers next to each other
+            dev.fill_cuda_graph_metadata(16, rows)
+            idx, ptr, _, _ = ref.fill_cuda_graph_metadata(16, rows)
+            assert dev._cg_kv_shared[16].tolist() == ref.shared_prefix_pages(idx, ptr), step
+            continue
         if kind == "share":
-            live = sorted(s for s in ids if s in ref.batch_to_blocks)
             if not live or sid in ref.batch_to_blocks:
                 continue
             p = rng.choice(live + [99])  # 99: not allocated (ValueError in both)
-            tokens = (ref.seq_len(p) if p in ref.batch_to_blocks else 0) + rng.choice([-1, 0, 1, 20])
+            tokens = (ref.seq_len(p) if p in ref.batch_to_blocks else 0) + rng.choice([-20, -5, -1, 0, 0, 1, 7, 20])
             name, args, kw = "allocate", (sid, max(tokens, 0)), {"prefix": p}
         elif kind == "alloc" and sid not in ref.batch_to_blocks:
             name, args, kw = "allocate", (sid, n), {}
@@ -262,7 +272,71 @@ def test_prefix_sharing_matches_oracle(seed):
         if step % 10 == 0 or err_ref:
             _same_state(dev, ref)
     _same_state(dev, ref)
+    assert len(ref.cow_pairs) > 5  # the sequence did exercise copies on write
     assert dev.pool_errors() == 0
+
+
+def test_copy_on_write_copies_every_layer_of_the_page():
+    """A sequence that shares a partial last page and then appends gets a private copy: a new
+    page id whose K/V, in every layer, equal the shared page's, while the shared page and its
+    other holder are untouched; a sequence allocated past a shared partial page copies it at
+    allocate; freeing the sharers returns the pages only they held."""
+    L, hkv, d = 3, 2, 64
+    m, ref = _pool(40, layers=L, hkv=hkv, d=d), RefKVCacheManager(40)
+    gen = torch.Generator().manual_seed(5)
+    m.kv_cache.copy_(torch.randn(m.kv_cache.shape, generator=gen).to(m.kv_cache.dtype))
+    before = m.kv_cache.clone()
+    for mm in (m, ref):
+        mm.allocate("p", 40)           # 3 pages, the last holds 8 tokens
+        mm.allocate("a", 40, prefix="p")
+        mm.allocate("b", 45, prefix="p")  # continues past p's partial page: copied at allocate
+    for mm in (m, ref):
+        mm.append_tokens("a", 1)          # into the shared page: copied first
+    _same_state(m, ref)
+    torch.cuda.synchronize()
+    pa, pb, pp = m.batch_to_blocks["a"], m.batch_to_blocks["b"], m.batch_to_blocks["p"]
+    assert pa[:2] == pp[:2] == pb[:2] and len({pa[2], pb[2], pp[2]}) == 3
+    for layer in range(L):
+        for copy in (pa[2], pb[2]):
+            assert torch.equal(m.kv_cache[layer, copy].view(torch.int16), before[layer, pp[2]].view(torch.int16))
+    # every page but the two copies holds what it held before
+    others = [x for x in range(40) if x not in (pa[2], pb[2])]
+    assert torch.equal(m.kv_cache[:, others].view(torch.int16), before[:, others].view(torch.int16))
+    for mm in (m, ref):
+        mm.free("p")
+        mm.free("a")
+    _same_state(m, ref)
+    assert m.pool_errors() == 0
+
+
+def test_device_steps_on_a_shared_last_page():
+    """begin_device_steps gives each row whose new tokens would go into a shared page its copy
+    first (in row order, as each row's first append would), then the steps run on the device:
+    page tables against the oracle doing the same copies and appends."""
+    m, ref = _pool(200, stride=8), RefKVCacheManager(200)
+    m.init_cuda_graph_buffers([8])
+    ref.init_cuda_graph_buffers([8])
+    for mm in (m, ref):
+        mm.allocate("p", 37)
+        mm.allocate("x", 37, prefix="p")
+        mm.allocate("y", 20, prefix="p")
+        mm.allocate("z", 64, prefix="p")
+    ids = ["p", "x", "y", "z"]
+    m.begin_device_steps(8, ids, steps=20)
+    ref.make_last_pages_private(ids)
+    for step in range(20):
+        m.advance_device_step(8)
+        m.device_step(8)
+        for sid in ids:
+            ref.append_tokens(sid, 1)
+        torch.cuda.synchronize()
+        idx, ptr, last, pos = ref.fill_cuda_graph_metadata(8, ids)
+        assert m._cg_kv_indptr[8].tolist() == ptr, step
+        assert m._cg_kv_indices[8][:len(idx)].tolist() == idx, step
+        assert m._cg_kv_last_page_len[8].tolist() == last, step
+    m.end_device_steps()
+    _same_state(m, ref)
+    assert m.pool_errors() == 0
 
 
 def test_uncached_append_matches_oracle_and_cached_path():

@@ -96,41 +96,58 @@ def test_seq_len_tracks_token_count():
 
 
 def test_prefix_sharing_hand_trace():
-    """The prefix extension on a 10-page pool, derived by hand: shared pages are the
-    prefix's full pages, never popped or pushed by the sequences that share them."""
+    """The sharing extension on a 10-page pool, derived by hand: shared pages (a partial last
+    page included), copies on write at allocate and at append, nested prefixes, and frees that
+    return only the pages no other list holds."""
     m = RefKVCacheManager(10)
-    assert m.allocate("p", 40) == [9, 8, 7]           # 2 full pages + 8 tokens
-    assert m.allocate("a", 40, prefix="p") == [9, 8, 6]  # shares [9, 8]; its own page 6
-    assert m.allocate("b", 32, prefix="p") == [9, 8]     # nothing of its own yet
-    assert m.batch_to_page_lengths["b"] == 16
-    m.append_tokens("b", 1)                              # 17th token of its last page: pops 5
-    assert m.batch_to_blocks["b"] == [9, 8, 5] and m.batch_to_page_lengths["b"] == 1
-    with pytest.raises(RuntimeError, match="p is the shared prefix of 2 live sequences"):
-        m.free("p")
-    with pytest.raises(ValueError, match="q not allocated"):
-        m.allocate("c", 40, prefix="q")
-    with pytest.raises(ValueError, match="shorter than its shared prefix"):
-        m.allocate("c", 31, prefix="p")
-    with pytest.raises(RuntimeError, match="Not enough KV cache blocks available"):
-        m.allocate("c", 32 + 16 * 6, prefix="p")  # 6 own pages, 5 free
-    assert m.free_blocks == [0, 1, 2, 3, 4]
+    assert m.allocate("p", 40) == [9, 8, 7]              # 2 full pages + 8 tokens
+    assert m.allocate("a", 40, prefix="p") == [9, 8, 7]  # all of p, its partial page too
+    assert m.allocate("b", 45, prefix="p") == [9, 8, 6]  # continues past p's partial page: copy
+    assert m.batch_to_page_lengths["b"] == 13
+    assert m.allocate("c", 20, prefix="p") == [9, 8]     # p's pages for its first 20 tokens
+    m.append_tokens("c", 1)                              # into the shared page 8: copy
+    assert m.batch_to_blocks["c"] == [9, 5] and m.batch_to_page_lengths["c"] == 5
+    m.append_tokens("a", 8)                              # copy of 7, then the page after
+    assert m.batch_to_blocks["a"] == [9, 8, 4, 3] and m.batch_to_page_lengths["a"] == 0
+    assert m.cow_pairs == [(7, 6), (8, 5), (7, 4)]
+    assert m.refs == {9: 4, 8: 3, 7: 1, 6: 1, 5: 1, 4: 1, 3: 1}
+    assert m.shared_prefix_pages(*m.get_append_metadata(["p", "a", "b", "c"])[:2]) == [0, 2, 2, 1]
+    m.free("p")                                          # only page 7 was p's alone
+    assert m.free_blocks == [0, 1, 2, 7]
+    assert m.allocate("d", 64, prefix="a") == [9, 8, 4, 7]  # nested: a's pages hold p's
     m.free("a")
-    assert m.free_blocks == [0, 1, 2, 3, 4, 6]
+    assert m.free_blocks == [0, 1, 2, 3]
     m.free("b")
-    m.free("p")
-    assert m.free_blocks == [0, 1, 2, 3, 4, 6, 5, 9, 8, 7]
-    # a prefix whose last page is partial shares only its full pages
-    m.allocate("p2", 20)                                  # pops 7, 8
-    assert m.allocate("d", 20, prefix="p2") == [7, 9]
+    assert m.free_blocks == [0, 1, 2, 3, 6]
+    with pytest.raises(ValueError, match="q not allocated"):
+        m.allocate("e", 40, prefix="q")
+    with pytest.raises(RuntimeError, match="Not enough KV cache blocks available"):
+        m.allocate("e", 16 * 10, prefix="d")             # 6 pages of its own, 5 free
+    m.free("c")
+    m.free("d")
+    assert m.free_blocks == [0, 1, 2, 3, 6, 5, 9, 8, 4, 7] and m.refs == {}
+    # append with the pool empty and a copy due: the reference's exception, nothing changed
+    m2 = RefKVCacheManager(2)
+    m2.allocate("x", 5)
+    m2.allocate("y", 5, prefix="x")
+    m2.append_tokens("y", 0)                             # no token: no copy
+    m2.allocate("z", 16)
+    with pytest.raises(RuntimeError, match="Not enough free blocks to append tokens"):
+        m2.append_tokens("x", 1)
+    assert m2.batch_to_blocks == {"x": [1], "y": [1], "z": [0]} and m2.refs == {1: 2, 0: 1}
 
 
-prefix_ops = st.lists(st.tuples(st.sampled_from(["alloc", "share", "append", "free"]), st.integers(0, 5),
+prefix_ops = st.lists(st.tuples(st.sampled_from(["alloc", "share", "share", "append", "free"]), st.integers(0, 5),
                                 st.integers(0, 70)), max_size=60)
 
 
 @settings(max_examples=200, deadline=None)
 @given(prefix_ops)
 def test_prefix_pool_invariants(seq):
+    """Under random allocate / share (nested, shorter and longer than the prefix) / append /
+    free: every page is either free or held, each count equals the lists that hold it, the
+    counts never rise along a list (the pages a free returns are a tail), copies on write pop
+    pages that were free, and lengths stay consistent."""
     P = 60
     m = RefKVCacheManager(P)
     for kind, sid, n in seq:
@@ -141,22 +158,22 @@ def test_prefix_pool_invariants(seq):
                 live = sorted(m.batch_to_blocks)
                 if live:
                     p = live[n % len(live)]
-                    m.allocate(sid, m.seq_len(p) + n % 20, prefix=p)
+                    m.allocate(sid, max(0, m.seq_len(p) + n % 40 - 20), prefix=p)
             elif kind == "append" and sid in m.batch_to_blocks:
-                m.append_tokens(sid, n)
+                m.append_tokens(sid, n % 20)
             elif kind == "free":
                 m.free(sid)
         except RuntimeError:
             pass
-        own = {b: pages[m.shared.get(b, (None, 0))[1]:] for b, pages in m.batch_to_blocks.items()}
-        flat = [p for pages in own.values() for p in pages]
-        # own pages are disjoint and conserved with the free list
-        assert len(flat) == len(set(flat))
-        assert sorted(flat + m.free_blocks) == list(range(P))
-        for b, (p, k) in m.shared.items():
-            # shared pages are the prefix's own leading pages, and the prefix is live
-            assert m.batch_to_blocks[b][:k] == m.batch_to_blocks[p][:k]
-            assert m.refs[p] >= 1
+        held = {}
         for b, pages in m.batch_to_blocks.items():
+            for pg in pages:
+                held[pg] = held.get(pg, 0) + 1
+        assert held == m.refs
+        assert not set(held) & set(m.free_blocks)
+        assert sorted(list(held) + m.free_blocks) == list(range(P))
+        for b, pages in m.batch_to_blocks.items():
+            counts = [m.refs[pg] for pg in pages]
+            assert counts == sorted(counts, reverse=True)
             if pages:
                 assert m.seq_len(b) == (len(pages) - 1) * 16 + m.batch_to_page_lengths[b]
