@@ -15,11 +15,17 @@
 //                                slot 8*(l/16) + e holds key 4*(l/16) + e of the first page for
 //                                e < 4 and of the second for e >= 4, which is where the softmax
 //                                left P and where two ds_read_b64_tr_b16 leave V^T
-// Pages go global -> LDS directly (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l),
-// three steps in flight, so no registers hold them on the way.  Each wave owns 32 rows
-// outright, so waves never combine.  An item that is one chunk of a
-// longer key range writes a partial (normalised rows plus running max and sum); the merge
-// kernel folds the partials of each split group.
+// Pages go global -> LDS directly (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l)
+// into rings of three K and three V stages, so no registers hold them on the way.  Each wave owns
+// 32 rows outright, so waves never combine.
+// Schedule: a step is a matrix phase (K . Q^T of step j and P.V of step j - 1, as a software
+// pipeline of eight-product units whose LDS operands are read one unit ahead) and a softmax
+// phase, each ending at a workgroup barrier; waves 4-7 run one phase behind waves 0-3, so each
+// SIMD (waves w and w + 4) overlaps one wave's matrix phase with the other's softmax.  Page ids
+// are read from the LDS page table a phase before they are needed (a lookup in the matrix phase
+// would wait behind the other waves' operand reads).
+// An item that is one chunk of a longer key range writes a partial (normalised rows plus
+// running max and sum); the merge kernel folds the partials of each split group.
 #include <type_traits>
 #include "attn_common.h"
 #include "mfma_common.h"
@@ -55,6 +61,45 @@ __device__ __forceinline__ void lds_copy16(const void* src, const char* dst) {
   const unsigned m0 = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+// A workgroup barrier that also ends the compiler's scheduling region, so that no instruction
+// moves between the phases it separates.
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+// Maxima without the canonicalising copies IEEE mode adds around fmaxf (the inputs are matrix-core
+// results or -inf, never signalling NaNs).
+__device__ __forceinline__ float max2f(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ float max_of(const float* v) {
+  static_assert(N == 16, "max_of");
+  const float a = max3f(max3f(v[0], v[1], v[2]), max3f(v[3], v[4], v[5]), max3f(v[6], v[7], v[8]));
+  const float b = max3f(max3f(v[9], v[10], v[11]), max3f(v[12], v[13], v[14]), v[15]);
+  return max2f(a, b);
+}
+// Maximum over the four 16-lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) by two lane swaps.
+__device__ __forceinline__ float max_across_groups(float x) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = max2f(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// The same copy from a wave-uniform base (an SGPR pair) plus a 32-bit per-lane byte offset.
+__device__ __forceinline__ void lds_copy16(const void* sbase, unsigned voff, const char* dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0) : "memory", "m0");
 }
 constexpr int kItem = 12;    // int32 fields per work item
 constexpr int kGroup = 8;    // int32 fields per split group
@@ -94,15 +139,14 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
   constexpr int STEPB = NP * TILEB;   // one step's pages
   constexpr int RPI = 64 / CPR;       // rows per 1 KB direct load (one 16-byte chunk per lane)
   constexpr int LPP = 16 / RPI;       // loads per page and K or V
-  constexpr int LPW = NP * 2 * LPP / 8;  // loads per wave per step
-  static_assert(NP * 2 * LPP % 8 == 0, "loads per wave");
+  constexpr int KL = NP * LPP / 8;    // K (and V) loads per wave per step
+  static_assert(NP * LPP % 8 == 0, "loads per wave");
   constexpr int TQ = kRows / G;       // query tokens per item
 
-  // three stages as distinct arrays (the step loop is unrolled by three): the compiler can then
-  // tell the stage being read from the stages being filled and does not wait for the latter
-  __shared__ __align__(16) char s_k0[STEPB], s_k1[STEPB], s_k2[STEPB];
-  __shared__ __align__(16) char s_v0[STEPB], s_v1[STEPB], s_v2[STEPB];
-  __shared__ int s_page[kMaxChunk / 16 + kStepPages];  // the chunk's page ids, -1 = absent
+  // rings of three stages for K and for V
+  __shared__ __align__(16) char s_k[3 * STEPB];
+  __shared__ __align__(16) char s_v[3 * STEPB];
+  __shared__ __align__(16) int s_page[kMaxChunk / 16 + kStepPages];  // the chunk's page ids, -1 = absent
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
@@ -147,40 +191,57 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     const int64_t pg = e >= 0 ? P.indices[e] : -1;
     s_page[i] = (pg >= 0 && pg < P.num_pages) ? (int)pg : -1;
   }
+  // V stage 2 starts zero-filled: the first M phase multiplies it by a zero P (uninitialised LDS
+  // could hold NaN bit patterns, and 0 * NaN is NaN)
+  for (int i = threadIdx.x; i < STEPB / 16; i += blockDim.x)
+    reinterpret_cast<uint4*>(s_v + 2 * STEPB)[i] = make_uint4(0, 0, 0, 0);
   // the Q loads are complete here; a compiler-visible vmcnt(0) (expcnt, lgkmcnt at their maxima)
   // tells the compiler so, which keeps it from waiting on them, and on every copy in flight,
   // inside the step loop
   __builtin_amdgcn_s_waitcnt(0x0F70);
   lds_barrier();
-  auto page_of = [&](int key) __attribute__((always_inline)) -> int {  // -1: absent page
-    return s_page[(key - k0) / 16];
+  // Step st's K (or V) pages into a stage: K wave-load wi (this wave: wi = wave * KL + x) covers
+  // RPI rows of page wi / LPP (the same page, my_page, for all of a wave's loads); lane l fills
+  // LDS slot l, i.e. row RPI*(wi % LPP) + l / CPR, position l % CPR, which holds the row's chunk
+  // position ^ swizzle(row).  The page id pg (wave-uniform, read from the table a phase ahead)
+  // gives the base and each lane adds its byte offset; absent pages (and, for V, keys past the
+  // chunk, per row) read zero rows.
+  static_assert(LPP % KL == 0, "a wave's loads of a step cover one page");
+  const int my_page = wave * KL / LPP;
+  // this wave's page of step st (a VGPR holding a uniform value; st clamped into the chunk)
+  auto page_id = [&](int st) __attribute__((always_inline)) -> int {
+    return s_page[min(st, nsteps - 1) * NP + my_page];
   };
-  // Step st's pages into stage buf: wave-load wi (this wave: wi = wave * LPW + x) covers RPI
-  // rows of one page's K or V; lane l fills LDS slot l, i.e. row RPI*(wi % LPP) + l / CPR,
-  // position l % CPR, which holds the row's chunk position ^ swizzle(row).
-  auto issue_step = [&](int st, char* kstage, char* vstage) __attribute__((always_inline)) {
+  const char* kbase = reinterpret_cast<const char*>(kc + hoff);
+  const char* vbase = reinterpret_cast<const char*>(vc + hoff);
+  const int64_t page_bytes = P.page_stride * (int64_t)sizeof(T);
+  auto issue_k = [&](int st, char* kstage, int pg) __attribute__((always_inline)) {
     const int kb = k0 + 16 * NP * st;
 #pragma unroll
-    for (int x = 0; x < LPW; ++x) {
-      const int wi = wave * LPW + x;
-      const int p = wi / (2 * LPP), kv = (wi / LPP) & 1, r0 = RPI * (wi % LPP);
-      const int row = r0 + lane / CPR, pos = lane % CPR;
-      const int pg = page_of(kb + 16 * p);
-      const int key = kb + 16 * p + row;
-      const void* src;
-      char* dst;
-      if (kv) {
-        const int col = pos ^ vswz<D>(row);
-        src = (pg < 0 || key >= k1) ? (const void*)(g_zero_rows + lane)
-                                    : (const void*)(vc + (int64_t)pg * P.page_stride + row * rowstride + hoff + 8 * col);
-        dst = vstage + p * TILEB + r0 * ROWB;
+    for (int x = 0; x < KL; ++x) {
+      const int wi = wave * KL + x;
+      const int p = wi / LPP, r0 = RPI * (wi % LPP);
+      const int row = r0 + lane / CPR, col = (lane % CPR) ^ kswz<D>(row);
+      char* dst = kstage + p * TILEB + r0 * ROWB;
+      if (pg >= 0) lds_copy16(kbase + pg * page_bytes, (unsigned)((row * rowstride + 8 * col) * sizeof(T)), dst);
+      else lds_copy16(g_zero_rows, (unsigned)(16 * lane), dst);
+    }
+  };
+  auto issue_v = [&](int st, char* vstage, int pg) __attribute__((always_inline)) {
+    const int kb = k0 + 16 * NP * st;
+#pragma unroll
+    for (int x = 0; x < KL; ++x) {
+      const int wi = wave * KL + x;
+      const int p = wi / LPP, r0 = RPI * (wi % LPP);
+      const int row = r0 + lane / CPR, col = (lane % CPR) ^ vswz<D>(row);
+      char* dst = vstage + p * TILEB + r0 * ROWB;
+      const unsigned voff = (unsigned)((row * rowstride + 8 * col) * sizeof(T));
+      if (pg >= 0 && kb + 16 * p + 16 <= k1) {
+        lds_copy16(vbase + pg * page_bytes, voff, dst);
       } else {
-        const int col = pos ^ kswz<D>(row);
-        src = (pg < 0) ? (const void*)(g_zero_rows + lane)
-                       : (const void*)(kc + (int64_t)pg * P.page_stride + row * rowstride + hoff + 8 * col);
-        dst = kstage + p * TILEB + r0 * ROWB;
+        const bool zero = pg < 0 || kb + 16 * p + row >= k1;
+        lds_copy16(zero ? (const void*)(g_zero_rows + lane) : (const void*)(vbase + pg * page_bytes + voff), dst);
       }
-      lds_copy16(src, dst);
     }
   };
 
@@ -213,63 +274,133 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
   lim_min = __builtin_amdgcn_readfirstlane(lim_min);
   const float scale = P.scale_log2;
 
-  // step st: compute on stage (ks, vs) = stage st % 3, refill stage (kn, vn) with step st + 2
-  auto do_step = [&](int st, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
-    // this wave's loads of step st are done (step st + 1's may still be in flight) ...
-    if (st + 1 < nsteps) wait_vmcnt<LPW>();
-    else wait_vmcnt<0>();
-    // ... and every wave's: step st is staged, and every wave is past step st - 1, whose
-    // stage is refilled next
-    lds_barrier();
-    if (st + 2 < nsteps) issue_step(st + 2, kn, vn);
-    const int kb = k0 + 16 * NP * st;
-    bool absent[NP];
-    bool full = kb + 16 * NP <= lim_min;  // (uniform)
+  // Ping-pong schedule.  A step is two phases: M(j) on the matrix cores (S^T = K . Q^T of step
+  // j, and O^T += V^T . P of step j - 1) and S(j) on the vector ALUs (the online softmax of step
+  // j's scores into P).  Every wave runs M(0) S(0) M(1) S(1) ... S(n-1) M(n), each phase ending
+  // at a workgroup barrier, and waves 4-7 start one phase after waves 0-3: each SIMD holds
+  // waves w and w + 4, so one runs a matrix phase while the other runs a softmax phase.
+  // Stage rings of three for K and for V: at M(j) every wave issues its share of K(j + 2) and
+  // V(j + 1).  Counting phases from the leading waves' M(0) = 0, K(j) is read in phases 2j and
+  // 2j + 1 and V(j) in 2j + 2 and 2j + 3, so the slot a refill issued at phase 2j or later
+  // overwrites has had its last read; and the refill is needed from phase 2j + 4, so each wave
+  // waits for its loads issued before its latest M phase ahead of the barrier that ends phase
+  // 2j + 3 (the leading waves' S(j + 1), the trailing waves' M(j + 1)).
+  f4 sacc[NP][2];    // S^T tiles of the step in flight: [key tile kt][row tile rt]
+  uint2 pb[NP][2];   // P of the previous step, packed as the B operand of P.V (zero before step 0)
 #pragma unroll
-    for (int kt = 0; kt < NP; ++kt) {
-      absent[kt] = page_of(kb + 16 * kt) < 0;
-      full = full && !absent[kt];
+  for (int kt = 0; kt < NP; ++kt)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) pb[kt][rt] = make_uint2(0, 0);
+  const int tr_row = 4 * lg + (lr >> 2);
+  // M(j): the page loads of later steps, then the products as a software pipeline of units of
+  // eight 16x16x32 products: units 0-3 are P.V of step j - 1 (pages 2u, 2u + 1 with u = unit / 2,
+  // output tiles 4 (unit % 2) .. + 3), units 4-7 are K . Q^T of step j (page unit - 4).  Each unit's
+  // LDS operands are read one unit ahead into the other half of a double buffer, and every unit
+  // ends the compiler's scheduling region, so reads stay one unit ahead of the products (which
+  // hides their latency) without holding more than two units of operands.
+  constexpr int MTU = MT / 2;  // output tiles per P.V unit
+  static_assert(MTU == KSTEPS, "a P.V unit and a K . Q^T unit take the same operand count");
+  uint4 opnd[2][KSTEPS];
+  auto read_unit = [&](int i, int buf, const char* ks, const char* vs) __attribute__((always_inline)) {
+    if (i < 4) {
+      const int u = i >> 1;
+      const char* tra = vs + (2 * u) * TILEB + tr_row * ROWB + (lr & 1) * 8;
+      const char* trb = tra + TILEB;
+#pragma unroll
+      for (int m = 0; m < MTU; ++m) {
+        const int mt = MTU * (i & 1) + m;
+        const int chunk = ((2 * mt + ((lr & 3) >> 1)) ^ vswz<D>(tr_row)) << 4;
+        const uint2 va = lds_read_tr16(tra + chunk), vb = lds_read_tr16(trb + chunk);
+        opnd[buf][m] = make_uint4(va.x, va.y, vb.x, vb.y);
+      }
+    } else {
+      const char* krow = ks + (i - 4) * TILEB + lr * ROWB;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+        opnd[buf][s] = *reinterpret_cast<const uint4*>(krow + (((4 * s + lg) ^ kswz<D>(lr)) << 4));
     }
-    // S^T tiles: [key tile kt][row tile rt]
-    f4 sacc[NP][2];
+  };
+  auto mma_unit = [&](int i, int buf) __attribute__((always_inline)) {
+    if (i < 4) {
+      const int u = i >> 1;
+      uint4 pp[2];
 #pragma unroll
-    for (int kt = 0; kt < NP; ++kt) {
-      const char* krow = ks + kt * TILEB + lr * ROWB;
+      for (int rt = 0; rt < 2; ++rt)
+        pp[rt] = make_uint4(pb[2 * u][rt].x, pb[2 * u][rt].y, pb[2 * u + 1][rt].x, pb[2 * u + 1][rt].y);
+#pragma unroll
+      for (int m = 0; m < MTU; ++m)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          o[rt][MTU * (i & 1) + m] = Mma<T>::qk(opnd[buf][m], pp[rt], o[rt][MTU * (i & 1) + m]);
+    } else {
+      const int kt = i - 4;
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const uint4 a = *reinterpret_cast<const uint4*>(krow + (((4 * s + lg) ^ kswz<D>(lr)) << 4));
+      for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = Mma<T>::qk(a, qr[rt][s], sacc[kt][rt]);
-      }
+        for (int rt = 0; rt < 2; ++rt) sacc[kt][rt] = Mma<T>::qk(opnd[buf][s], qr[rt][s], sacc[kt][rt]);
     }
+  };
+  // Every M phase runs all eight units, so the pipeline has no branches: at j = 0, P.V multiplies
+  // the zero P it starts with by the zero-filled V stage 2 and adds exactly +0 to O; at
+  // j = nsteps, K . Q^T reads a stale K stage and its scores are never used.  Unit i's operands go
+  // to double-buffer half i % 2.
+  auto products = [&](const char* ks, const char* vs) __attribute__((always_inline)) {
+    read_unit(0, 0, ks, vs);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + 1 < 8) read_unit(i + 1, (i + 1) & 1, ks, vs);
+      mma_unit(i, i & 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert(NP == 4, "the product pipeline is written for four pages a step");
+  // Page ids reach the phases a phase early, so that no lookup waits behind the bulk LDS reads of
+  // the other waves: pk_next / pv_next (uniform) are the pages this wave loads at its next M phase
+  // (K of step j + 2, V of step j + 1 at M(j)); step_pages holds step j's four page ids for S(j).
+  int pk_next = 0, pv_next = 0;
+  int4 step_pages;
+  auto phase_m = [&](int j, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
+    step_pages = *reinterpret_cast<const int4*>(s_page + min(j, nsteps - 1) * NP);
+    if (j + 2 < nsteps) issue_k(j + 2, kn, pk_next);
+    if (j + 1 < nsteps) issue_v(j + 1, vn, pv_next);
+    products(ks, vs);
+  };
+  auto phase_s = [&](int j) __attribute__((always_inline)) {
+    // the next M phase's pages, read now and made scalar at the end of this phase
+    const int pk_raw = page_id(j + 3), pv_raw = page_id(j + 2);
+    const int kb = k0 + 16 * NP * j;
+    bool absent[NP];
+    absent[0] = __builtin_amdgcn_readfirstlane(step_pages.x) < 0;
+    absent[1] = __builtin_amdgcn_readfirstlane(step_pages.y) < 0;
+    absent[2] = __builtin_amdgcn_readfirstlane(step_pages.z) < 0;
+    absent[3] = __builtin_amdgcn_readfirstlane(step_pages.w) < 0;
+    bool full = kb + 16 * NP <= lim_min;  // (uniform)
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) full = full && !absent[kt];
     // online softmax per row tile on the raw scores (the scale is folded into the exponent's
-    // FMA; it is positive, so maxima commute with it); P packed as the B operand of P.V
-    uint2 pb[NP][2];
+    // FMA; it is positive, so maxima commute with it)
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float sv[NP][4];
-      float cmax = -INFINITY;
-      if (full) {
-#pragma unroll
-        for (int kt = 0; kt < NP; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[kt][rt][i];
-      } else {
+      // masked scores (causal limit, keys past the chunk, absent pages) become -inf in place
+      if (!full) {
 #pragma unroll
         for (int kt = 0; kt < NP; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kb + 16 * kt + 4 * lg + i;
-            sv[kt][i] = (key < lim[rt] && !absent[kt]) ? sacc[kt][rt][i] : -INFINITY;
+            if (!(key < lim[rt] && !absent[kt])) sacc[kt][rt][i] = -INFINITY;
           }
       }
+      float sv[NP * 4];
 #pragma unroll
       for (int kt = 0; kt < NP; ++kt)
-        cmax = fmaxf(cmax, fmaxf(fmaxf(sv[kt][0], sv[kt][1]), fmaxf(sv[kt][2], sv[kt][3])));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[4 * kt + i] = sacc[kt][rt][i];
+      float cmax = max_of<NP * 4>(sv);
+      cmax = max_across_groups(cmax);
       const float cms = cmax * scale;
       const bool grow = cms > m[rt] + kLazyMax;  // (false while every score so far is masked)
       if (__ballot(grow)) {
@@ -281,45 +412,61 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
         m[rt] = mnew;
       }
       const float nmuse = m[rt] == -INFINITY ? 0.f : -m[rt];
-      float psum = 0.f;
+      float psum[4];
 #pragma unroll
       for (int kt = 0; kt < NP; ++kt) {
         float pr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kt][i], scale, nmuse));
-          psum += pr[i];
+          pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[4 * kt + i], scale, nmuse));
+          psum[i] = kt == 0 ? pr[i] : psum[i] + pr[i];
         }
         pb[kt][rt] = make_uint2(Mma<T>::pack(pr[0], pr[1]), Mma<T>::pack(pr[2], pr[3]));
       }
-      lsum[rt] += psum;
+      lsum[rt] += (psum[0] + psum[1]) + (psum[2] + psum[3]);
     }
-    // O^T += V^T . P, two pages per 16x16x32 product
-    const int tr_row = 4 * lg + (lr >> 2);
-#pragma unroll
-    for (int u = 0; u < NP / 2; ++u) {
-      const char* tra = vs + (2 * u) * TILEB + tr_row * ROWB + (lr & 1) * 8;
-      const char* trb = tra + TILEB;
-      uint4 pp[2];
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        pp[rt] = make_uint4(pb[2 * u][rt].x, pb[2 * u][rt].y, pb[2 * u + 1][rt].x, pb[2 * u + 1][rt].y);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int chunk = ((2 * mt + ((lr & 3) >> 1)) ^ vswz<D>(tr_row)) << 4;
-        const uint2 va = lds_read_tr16(tra + chunk), vb = lds_read_tr16(trb + chunk);
-        const uint4 vt = make_uint4(va.x, va.y, vb.x, vb.y);
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) o[rt][mt] = Mma<T>::qk(vt, pp[rt], o[rt][mt]);
-      }
+    __builtin_amdgcn_sched_barrier(0);
+    pk_next = __builtin_amdgcn_readfirstlane(pk_raw);
+    pv_next = __builtin_amdgcn_readfirstlane(pv_raw);
+  };
+  // this wave's loads issued before its M(j) are complete (M(j)'s may stay in flight)
+  auto wait_before = [&](int j) __attribute__((always_inline)) {
+    if (j + 2 < nsteps) wait_vmcnt<2 * KL>();
+    else wait_vmcnt<0>();
+  };
+  const bool lead = wave < 4;
+  auto round = [&](int j, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
+    phase_m(j, ks, vs, kn, vn);
+    if (!lead) wait_before(j);
+    phase_barrier();
+    if (j < nsteps) {
+      phase_s(j);
+      if (lead) wait_before(j);
+      phase_barrier();
     }
   };
-  if (nsteps > 0) issue_step(0, s_k0, s_v0);
-  if (nsteps > 1) issue_step(1, s_k1, s_v1);
-  for (int st = 0; st < nsteps; st += 3) {
-    do_step(st, s_k0, s_v0, s_k2, s_v2);
-    if (st + 1 < nsteps) do_step(st + 1, s_k1, s_v1, s_k0, s_v0);
-    if (st + 2 < nsteps) do_step(st + 2, s_k2, s_v2, s_k1, s_v1);
+  if (nsteps > 0) {
+    issue_k(0, s_k, __builtin_amdgcn_readfirstlane(page_id(0)));
+    issue_v(0, s_v, __builtin_amdgcn_readfirstlane(page_id(0)));
+    pk_next = __builtin_amdgcn_readfirstlane(page_id(2));
+    pv_next = __builtin_amdgcn_readfirstlane(page_id(1));
+    if (nsteps > 1) {
+      issue_k(1, s_k + STEPB, __builtin_amdgcn_readfirstlane(page_id(1)));
+      wait_vmcnt<2 * KL>();
+    } else {
+      wait_vmcnt<KL>();
+    }
+    phase_barrier();  // K(0) staged
+    if (!lead) phase_barrier();  // the trailing waves' idle first phase
+    int cs = 0;  // stage of step j (j % 3)
+#pragma unroll 1
+    for (int j = 0; j <= nsteps; ++j) {
+      const int ns = cs == 2 ? 0 : cs + 1;  // (j + 1) % 3
+      const int ps = cs == 0 ? 2 : cs - 1;  // (j + 2) % 3, also (j - 1) % 3
+      round(j, s_k + cs * STEPB, s_v + ps * STEPB, s_k + ps * STEPB, s_v + ns * STEPB);
+      cs = ns;
+    }
+    if (lead) phase_barrier();  // the leading waves' idle last phase
   }
 
   // ---- rows out: normalised output rows, or the partial of a split group
