@@ -210,6 +210,41 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each XCD a
   // run of consecutive ranges keeps a split sequence's partials mostly on one L2.
   const int w0 = (N0 % 8 == 0) ? (int)(blockIdx.x % 8) * (N0 / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  // The first range's head (round 1), its segment records and its first 256 page ids are
+  // requested before anything else: none depends on another, and the set-up code below (several
+  // hundred instructions) then runs while they are in flight.
+  int hv0 = 0, pv0 = 0;
+  const bool early = w0 < P.r_cap;
+  if (early) {
+    const int32_t* head0 = P.sched_head + (int64_t)w0 * kHeadWords;
+    const int32_t* rec0 = P.sched + (int64_t)w0 * kRecStride;
+    hv0 = head0[lane];
+    pv0 = head0[kHeadPidOff + lane];
+    if (wave == 0) dma16(rec0 + kRecSegOff + 4 * lane, reinterpret_cast<const char*>(s_seg));
+    if (wave == 1 % W) dma16(rec0 + kRecPidOff + 4 * lane, reinterpret_cast<const char*>(s_pid));
+  }
+  // ... and, once the head is in, this wave's first unit: HBM then streams the first pages while
+  // the set-up code runs (the range loop takes them over as its first unit)
+  int cpid0 = 0;
+  bool unit0 = false;
+  if (early) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the head is in (compiler-visible vmcnt(0))
+    int len0 = __builtin_amdgcn_readlane(hv0, kHdrLen);
+    len0 = len0 < 0 ? 0 : (len0 > kRangePages ? kRangePages : len0);
+    int nseg0 = __builtin_amdgcn_readlane(hv0, kHdrNseg);
+    nseg0 = nseg0 < 0 ? 0 : (nseg0 > len0 ? len0 : nseg0);
+    bool plain = w0 < __builtin_amdgcn_readlane(hv0, kHdrRanges) && nseg0 > 0;
+    if constexpr (CASC) plain = plain && !__builtin_amdgcn_readlane(hv0, kHdrPrefix);
+    const int pi0 = active ? j : len0;
+    if (plain && pi0 < len0) {
+      const int raw = __builtin_amdgcn_readlane(pv0, pi0);
+      cpid0 = pid_page(raw);
+      const int64_t pg = page_ok(cpid0) ? cpid0 : 0;
+      issue_tile(kc, pg, kbuf, false, -1, !pid_cached(raw));
+      issue_tile(vc, pg, vbuf, true, -1, !pid_cached(raw));
+      unit0 = true;
+    }
+  }
   int nsplit = 0;
 
   // Deferred arrivals of split segments: every wave waits for its own partial stores, then one
@@ -464,8 +499,10 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     const int32_t* head = P.sched_head + (int64_t)w * kHeadWords;
     lds_barrier();  // the previous range's readers of s_pid / s_seg / the query rows are done
     // ---- round 1: the range's head: header and first segments (words 0..63), first 64 page ids
-    const int hv = head[lane];
-    const int pv = head[kHeadPidOff + lane];
+    // (the first range's were requested at the start, with its first two round-2 jobs)
+    const bool first = early && w == w0;
+    const int hv = first ? hv0 : head[lane];
+    const int pv = first ? pv0 : head[kHeadPidOff + lane];
     const int rr = __builtin_amdgcn_readlane(hv, kHdrRanges);
     rmax = rr < rmax ? rr : rmax;
     int len = __builtin_amdgcn_readlane(hv, kHdrLen);
@@ -474,8 +511,14 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     nseg = nseg < 0 ? 0 : (nseg > len ? len : nseg);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // round 1 complete (compiler-visible vmcnt(0))
     if (w >= rmax) break;
+    // the early copies into s_seg / s_pid stand for this range's first two round-2 jobs, unless a
+    // prefix item carried by the range has since reused those arrays
+    bool early_jobs = first;
     if constexpr (CASC) {
-      if (__builtin_amdgcn_readlane(hv, kHdrPrefix)) prefix_item(w);
+      if (__builtin_amdgcn_readlane(hv, kHdrPrefix)) {
+        prefix_item(w);
+        early_jobs = false;
+      }
     }
     if (nseg == 0) continue;
     // segment s < kHeadSegs from the round-1 registers
@@ -493,6 +536,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     const int nqj = (qchunks + 63) / 64;
     const int njobs = 1 + npj + nqj;
     for (int k = wave; k < njobs; k += W) {
+      if (early_jobs && k <= 1) continue;  // (issued at the start)
       if (k == 0) {
         dma16(rec + kRecSegOff + 4 * lane, reinterpret_cast<const char*>(s_seg));
       } else if (k <= npj) {
@@ -515,14 +559,19 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     int pi = active ? j : len;  // this wave's current page (range page index)
     int cpid = 0;
     bool have = pi < len;
-    if (have) {
+    // (the first range's first unit went out at the start, before these copies: then every
+    // copy is waited for, the unit included)
+    const bool issued = first && unit0;
+    if (issued) {
+      cpid = cpid0;
+    } else if (have) {
       const int raw = __builtin_amdgcn_readlane(pv, pi);
       cpid = pid_page(raw);
       const int64_t pg = page_ok(cpid) ? cpid : 0;
       issue_tile(kc, pg, kbuf, false, -1, !pid_cached(raw));
       issue_tile(vc, pg, vbuf, true, -1, !pid_cached(raw));
     }
-    if (have) wait_vm<2 * NI>(); else wait_vm<0>();
+    if (have && !issued) wait_vm<2 * NI>(); else wait_vm<0>();
     lds_barrier();
 
     // ---- per-segment state

@@ -109,3 +109,49 @@ def test_full_size_step_qwen_36_layers(device_steps):
                 _check_layer(loop, layer, rows, idx, ptr, last)
         loop.retire()
     assert loop.mgr.pool_errors() == 0
+
+
+def test_full_size_cascade_and_hint_match_plain():
+    """Qwen2.5-3B shape, batch 128 on a 2048-token shared prefix: the cascade plan (prefix items
+    carried by ranges that also hold suffix pages) and the shared-page hint give the plain plan's
+    outputs, and rows of all three match the oracle."""
+    loop = workloads.SharedPrefixDecodeLoop(DEV, layers=1, max_steps=2)
+    loop.begin_step()
+    loop.mgr.append_paged_kv_cache_cuda_graph(loop.k[0], loop.v[0], loop.batch, 0)
+    torch.cuda.synchronize()
+    m, w, B = loop.mgr, loop.wrapper, loop.batch
+    outs = {}
+    items = {}
+    for mode in ("plain", "hint", "cascade"):
+        print(f"full-size shared prefix: {mode}", flush=True)
+        w.plan(m._cg_kv_indptr[B], m._cg_kv_indices[B], m._cg_kv_last_page_len[B], loop.hq, loop.hkv, loop.d, 16,
+               q_data_type=loop.dtype, kv_shared_pages=m._cg_kv_shared[B] if mode != "plain" else None,
+               cascade=mode == "cascade")
+        out = torch.empty_like(loop.out[0])
+        w.run(loop.q[0], m.kv_cache[0], out=out)
+        torch.cuda.synchronize()
+        outs[mode] = out.float()
+        # the plan's global header (after the per-sequence words): [ranges, ..., prefix items]
+        off = (4 * B + 255) // 256 * 256
+        items[mode] = w._workspace[off:off + 32].view(torch.int32).tolist()[4]
+    assert items["plain"] == 0 and items["cascade"] > 0, items
+    assert torch.isfinite(outs["cascade"]).all()
+    torch.testing.assert_close(outs["hint"], outs["plain"], atol=0, rtol=0)
+    # the plans differ only in fp32 summation order (3e-5 apart at this shape); a suffix read
+    # through the wrong page list lands ~7e-3 away
+    torch.testing.assert_close(outs["cascade"], outs["plain"], atol=5e-4, rtol=0)
+    idx = m._cg_kv_indices[B].tolist()
+    ptr = m._cg_kv_indptr[B].tolist()
+    last = m._cg_kv_last_page_len[B].tolist()
+    cache = m.kv_cache[0]
+    for r in (0, 37, 64, 127):
+        pages = torch.tensor(idx[ptr[r]:ptr[r + 1]], dtype=torch.long, device=DEV)
+        L = (len(pages) - 1) * 16 + last[r]
+        kv = cache[pages].float().cpu().numpy()
+        k = kv[:, 0].reshape(-1, loop.hkv, loop.d)[:L]
+        v = kv[:, 1].reshape(-1, loop.hkv, loop.d)[:L]
+        q = loop.q[0, r:r + 1].float().cpu().numpy().astype(np.float64)
+        ref = kv_ref._attend(q, k, v, [L], loop.d ** -0.5)[0]
+        for mode in ("plain", "cascade"):
+            np.testing.assert_allclose(outs[mode][r].cpu().numpy(), ref, atol=2e-3, rtol=1e-2,
+                                       err_msg=f"{mode} row {r}")
