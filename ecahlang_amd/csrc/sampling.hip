@@ -96,7 +96,7 @@ struct Row {
 };
 
 __device__ __forceinline__ float block_max(float v, float* red) {
-  v = wave_max(v);
+  v = wave_max_f32(v);
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   __syncthreads();
   if (l == 0) red[w] = v;
@@ -105,11 +105,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   for (int i = 0; i < kThreads / 64; ++i) r = fmaxf(r, red[i]);
   return r;
 }
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { return wave_sum_u64_dpp(v); }
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
   v = wave_sum_u64(v);
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -434,7 +430,7 @@ struct SliceLoad {
 };
 
 __device__ __forceinline__ float block_max256(float v, float* red) {
-  v = wave_max(v);
+  v = wave_max_f32(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -576,16 +572,14 @@ __global__ __launch_bounds__(kSplitThreads) void split_sample_kernel(const T* lo
 }
 
 __device__ __forceinline__ int block_sum_i256(int v, int* red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  v = wave_sum_i32(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   return red[0] + red[1] + red[2] + red[3];
 }
 __device__ __forceinline__ uint32_t block_max_u256(uint32_t v, uint32_t* red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  v = wave_max_u32(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -721,16 +715,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logi
   // one wave merges (shuffle reductions, no workgroup barriers)
   if (threadIdx.x >= kWave) return;
   const int lane = threadIdx.x;
-  auto wsum_i = [](int v) __attribute__((always_inline)) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-  };
-  auto wmax_u = [](uint32_t v) __attribute__((always_inline)) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-    return v;
-  };
+  auto wsum_i = [](int v) __attribute__((always_inline)) { return wave_sum_i32(v); };
+  auto wmax_u = [](uint32_t v) __attribute__((always_inline)) { return wave_max_u32(v); };
   uint32_t ck[kMergeRegs];
   int cidx[kMergeRegs];
 #pragma unroll
