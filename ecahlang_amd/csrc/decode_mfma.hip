@@ -440,8 +440,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         }
         float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                            fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        cmax = max_across_groups(cmax);
         const float cms = cmax * scale;
         const bool grow = cms > pm[k] + kLazyMax;
         if (__ballot(grow)) {
@@ -470,8 +469,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     // each block's columns: this head's share of one part of each of its sequences
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      float ltot = pl[k] + __shfl_xor(pl[k], 16, 64);
-      ltot += __shfl_xor(ltot, 32, 64);
+      const float ltot = sum_across_groups(pl[k]);
       if (ok[k]) {
         const int64_t slot = (int64_t)sgk[k].slot0 + sgk[k].part;
         const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
@@ -630,8 +628,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     };
 
     auto end_segment = [&]() __attribute__((always_inline)) {
-      float ltot = lsum + __shfl_xor(lsum, 16, 64);
-      ltot += __shfl_xor(ltot, 32, 64);
+      const float ltot = sum_across_groups(lsum);
       const bool whole = sg.nparts == 1;
       float M = m, L = ltot;
       if (J > 1) {
@@ -781,8 +778,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[i] = (4 * lg + i < nv) ? sacc[i] : -INFINITY;
       float cmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      cmax = max_across_groups(cmax);
       const float cms = cmax * scale;
       const bool grow = cms > m + kLazyMax;  // (false while every score so far is masked)
       if (__ballot(grow)) {

@@ -88,5 +88,42 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   return u;
 }
 
+// Maxima without the canonicalising copies IEEE mode adds around fmaxf (the inputs are matrix-core
+// results or -inf, never signalling NaNs).
+__device__ __forceinline__ float max2f(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ float max_of(const float* v) {
+  static_assert(N == 16, "max_of");
+  const float a = max3f(max3f(v[0], v[1], v[2]), max3f(v[3], v[4], v[5]), max3f(v[6], v[7], v[8]));
+  const float b = max3f(max3f(v[9], v[10], v[11]), max3f(v[12], v[13], v[14]), v[15]);
+  return max2f(a, b);
+}
+// Maximum and sum over the four 16-lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) by two lane
+// swaps in registers (v_permlane16_swap: odd rows with even rows; v_permlane32_swap: the two
+// halves), where a shuffle would take two LDS round trips.  Every lane gets the result; all 64
+// lanes must be active.  The sum adds l ^ 16 first, then l ^ 32, as a shuffle-based
+// x + x^16, then + ^32 does, with the same operands, so it is bit-identical to that.
+__device__ __forceinline__ float max_across_groups(float x) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = max2f(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_across_groups(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+}
+
 }  // namespace mfma
 }  // namespace pkv

@@ -8,7 +8,7 @@
 //   item = (request, KV head, 256 / g query tokens, a chunk [k0, k1) of the keys they see)
 // A workgroup of 8 waves owns the item's 256 query rows (row r = token r / g, head r % g of the
 // KV head's group), so every staged K/V page serves all 256 rows.  Per 64 keys (four pages),
-// staged in LDS by all threads in a ring of three stages:
+// staged in LDS by all threads:
 //   S^T[key][row] = K . Q^T      v_mfma_f32_16x16x32, A = K from LDS, B = Q in registers
 //   online softmax per row in the accumulator layout (lane = row l % 16, keys 4*(l/16) + i)
 //   O^T[dim][row] += V^T . P     v_mfma_f32_16x16x32 over two pages at a time: the reduction
@@ -68,32 +68,6 @@ __device__ __forceinline__ void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
   __builtin_amdgcn_sched_barrier(0);
-}
-// Maxima without the canonicalising copies IEEE mode adds around fmaxf (the inputs are matrix-core
-// results or -inf, never signalling NaNs).
-__device__ __forceinline__ float max2f(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-template <int N>
-__device__ __forceinline__ float max_of(const float* v) {
-  static_assert(N == 16, "max_of");
-  const float a = max3f(max3f(v[0], v[1], v[2]), max3f(v[3], v[4], v[5]), max3f(v[6], v[7], v[8]));
-  const float b = max3f(max3f(v[9], v[10], v[11]), max3f(v[12], v[13], v[14]), v[15]);
-  return max2f(a, b);
-}
-// Maximum over the four 16-lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) by two lane swaps.
-__device__ __forceinline__ float max_across_groups(float x) {
-  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = max2f(__uint_as_float(h[0]), __uint_as_float(h[1]));
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // The same copy from a wave-uniform base (an SGPR pair) plus a 32-bit per-lane byte offset.
 __device__ __forceinline__ void lds_copy16(const void* sbase, unsigned voff, const char* dst) {
