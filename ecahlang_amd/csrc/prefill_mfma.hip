@@ -52,16 +52,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// One wave-wide 16-byte-per-lane copy global -> LDS: lane l's 16 bytes at src (per lane) land at
-// LDS byte dst + 16 * l (dst uniform across the wave, passed in M0).  Written as inline assembly
-// so that the compiler does not track it: the caller orders it with explicit vmcnt waits and
-// barriers (the compiler cannot tell which LDS array a later transposed read touches and would
-// otherwise wait for every copy in flight, draining the prefetch pipeline).
-__device__ __forceinline__ void lds_copy16(const void* src, const char* dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
-}
 // A workgroup barrier that also ends the compiler's scheduling region, so that no instruction
 // moves between the phases it separates.
 __device__ __forceinline__ void phase_barrier() {
@@ -69,11 +59,18 @@ __device__ __forceinline__ void phase_barrier() {
   lds_barrier();
   __builtin_amdgcn_sched_barrier(0);
 }
-// The same copy from a wave-uniform base (an SGPR pair) plus a 32-bit per-lane byte offset.
-__device__ __forceinline__ void lds_copy16(const void* sbase, unsigned voff, const char* dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
+// One wave-wide 16-byte-per-lane copy global -> LDS: lane l's 16 bytes at sbase + voff (a
+// wave-uniform base in an SGPR pair plus a 32-bit per-lane byte offset) land at LDS byte
+// m0 + 16 * l (m0 uniform).  Written as inline assembly so that the compiler does not track it:
+// the caller orders it with explicit vmcnt waits and barriers (the compiler cannot tell which LDS
+// array a later transposed read touches and would otherwise wait for every copy in flight,
+// draining the prefetch pipeline).
+__device__ __forceinline__ void lds_copy16(const void* sbase, unsigned voff, unsigned m0) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0) : "memory", "m0");
+}
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ unsigned lds_addr(const char* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
 }
 constexpr int kItem = 12;    // int32 fields per work item
 constexpr int kGroup = 8;    // int32 fields per split group
@@ -189,33 +186,37 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
   const char* kbase = reinterpret_cast<const char*>(kc + hoff);
   const char* vbase = reinterpret_cast<const char*>(vc + hoff);
   const int64_t page_bytes = P.page_stride * (int64_t)sizeof(T);
-  auto issue_k = [&](int st, char* kstage, int pg) __attribute__((always_inline)) {
-    const int kb = k0 + 16 * NP * st;
+  // (branch-free: the base and the offsets are selected, so the copies can sit between the
+  // products of the matrix phase; kstage / vstage are LDS byte addresses)
+  const char* const zero_rows = reinterpret_cast<const char*>(g_zero_rows);
+  auto issue_k = [&](int st, unsigned kstage, int pg) __attribute__((always_inline)) {
+    const bool have = pg >= 0;
+    const char* base = have ? kbase + pg * page_bytes : zero_rows;
 #pragma unroll
     for (int x = 0; x < KL; ++x) {
       const int wi = wave * KL + x;
       const int p = wi / LPP, r0 = RPI * (wi % LPP);
       const int row = r0 + lane / CPR, col = (lane % CPR) ^ kswz<D>(row);
-      char* dst = kstage + p * TILEB + r0 * ROWB;
-      if (pg >= 0) lds_copy16(kbase + pg * page_bytes, (unsigned)((row * rowstride + 8 * col) * sizeof(T)), dst);
-      else lds_copy16(g_zero_rows, (unsigned)(16 * lane), dst);
+      const unsigned off = have ? (unsigned)((row * rowstride + 8 * col) * sizeof(T)) : 16u * lane;
+      lds_copy16(base, off, kstage + p * TILEB + r0 * ROWB);
     }
   };
-  auto issue_v = [&](int st, char* vstage, int pg) __attribute__((always_inline)) {
+  // V rows at or past the chunk's end must not be NaN (their P is 0, and 0 * NaN is NaN): in a
+  // page that the chunk ends inside, they repeat the page's last row inside the chunk; a page
+  // entirely past the end, or absent, reads zero rows.
+  auto issue_v = [&](int st, unsigned vstage, int pg) __attribute__((always_inline)) {
     const int kb = k0 + 16 * NP * st;
 #pragma unroll
     for (int x = 0; x < KL; ++x) {
       const int wi = wave * KL + x;
       const int p = wi / LPP, r0 = RPI * (wi % LPP);
       const int row = r0 + lane / CPR, col = (lane % CPR) ^ vswz<D>(row);
-      char* dst = vstage + p * TILEB + r0 * ROWB;
-      const unsigned voff = (unsigned)((row * rowstride + 8 * col) * sizeof(T));
-      if (pg >= 0 && kb + 16 * p + 16 <= k1) {
-        lds_copy16(vbase + pg * page_bytes, voff, dst);
-      } else {
-        const bool zero = pg < 0 || kb + 16 * p + row >= k1;
-        lds_copy16(zero ? (const void*)(g_zero_rows + lane) : (const void*)(vbase + pg * page_bytes + voff), dst);
-      }
+      const int vr = k1 - kb - 16 * p;  // rows of this page inside the chunk (uniform)
+      const bool have = pg >= 0 && vr > 0;
+      const char* base = have ? vbase + pg * page_bytes : zero_rows;
+      const int rs = min(row, vr - 1);
+      const unsigned off = have ? (unsigned)((rs * rowstride + 8 * col) * sizeof(T)) : 16u * lane;
+      lds_copy16(base, off, vstage + p * TILEB + r0 * ROWB);
     }
   };
 
@@ -320,8 +321,8 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
   // the zero P it starts with by the zero-filled V stage 2 and adds exactly +0 to O; at
   // j = nsteps, K . Q^T reads a stale K stage and its scores are never used.  Unit i's operands go
   // to double-buffer half i % 2.
+  // (the caller has read unit 0's operands)
   auto products = [&](const char* ks, const char* vs) __attribute__((always_inline)) {
-    read_unit(0, 0, ks, vs);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_barrier(0);
@@ -336,8 +337,10 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
   // (K of step j + 2, V of step j + 1 at M(j)); step_pages holds step j's four page ids for S(j).
   int pk_next = 0, pv_next = 0;
   int4 step_pages;
-  auto phase_m = [&](int j, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
+  // (the copies are issued while the first unit's operand reads are in flight)
+  auto phase_m = [&](int j, const char* ks, const char* vs, unsigned kn, unsigned vn) __attribute__((always_inline)) {
     step_pages = *reinterpret_cast<const int4*>(s_page + min(j, nsteps - 1) * NP);
+    read_unit(0, 0, ks, vs);
     if (j + 2 < nsteps) issue_k(j + 2, kn, pk_next);
     if (j + 1 < nsteps) issue_v(j + 1, vn, pv_next);
     products(ks, vs);
@@ -359,14 +362,15 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       // masked scores (causal limit, keys past the chunk, absent pages) become -inf in place
+      // (key kb + 16 kt + 4 lg + i is below the limit iff 16 kt + i < rem: compares with
+      // immediates, all inside the branch)
       if (!full) {
+        const int rem = lim[rt] - kb - 4 * lg;
 #pragma unroll
         for (int kt = 0; kt < NP; ++kt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kb + 16 * kt + 4 * lg + i;
-            if (!(key < lim[rt] && !absent[kt])) sacc[kt][rt][i] = -INFINITY;
-          }
+          for (int i = 0; i < 4; ++i)
+            if (!(16 * kt + i < rem && !absent[kt])) sacc[kt][rt][i] = -INFINITY;
       }
       float sv[NP * 4];
 #pragma unroll
@@ -409,7 +413,7 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     else wait_vmcnt<0>();
   };
   const bool lead = wave < 4;
-  auto round = [&](int j, const char* ks, const char* vs, char* kn, char* vn) __attribute__((always_inline)) {
+  auto round = [&](int j, const char* ks, const char* vs, unsigned kn, unsigned vn) __attribute__((always_inline)) {
     phase_m(j, ks, vs, kn, vn);
     if (!lead) wait_before(j);
     phase_barrier();
@@ -420,12 +424,13 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     }
   };
   if (nsteps > 0) {
-    issue_k(0, s_k, __builtin_amdgcn_readfirstlane(page_id(0)));
-    issue_v(0, s_v, __builtin_amdgcn_readfirstlane(page_id(0)));
+    const unsigned sk = lds_addr(s_k), sv = lds_addr(s_v);
+    issue_k(0, sk, __builtin_amdgcn_readfirstlane(page_id(0)));
+    issue_v(0, sv, __builtin_amdgcn_readfirstlane(page_id(0)));
     pk_next = __builtin_amdgcn_readfirstlane(page_id(2));
     pv_next = __builtin_amdgcn_readfirstlane(page_id(1));
     if (nsteps > 1) {
-      issue_k(1, s_k + STEPB, __builtin_amdgcn_readfirstlane(page_id(1)));
+      issue_k(1, sk + STEPB, __builtin_amdgcn_readfirstlane(page_id(1)));
       wait_vmcnt<2 * KL>();
     } else {
       wait_vmcnt<KL>();
@@ -437,7 +442,7 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
     for (int j = 0; j <= nsteps; ++j) {
       const int ns = cs == 2 ? 0 : cs + 1;  // (j + 1) % 3
       const int ps = cs == 0 ? 2 : cs - 1;  // (j + 2) % 3, also (j - 1) % 3
-      round(j, s_k + cs * STEPB, s_v + ps * STEPB, s_k + ps * STEPB, s_v + ns * STEPB);
+      round(j, s_k + cs * STEPB, s_v + ps * STEPB, sk + ps * STEPB, sv + ns * STEPB);
       cs = ns;
     }
     if (lead) phase_barrier();  // the leading waves' idle last phase
