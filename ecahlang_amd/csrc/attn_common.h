@@ -138,64 +138,73 @@ constexpr int kMergeRegs = 8;  // segments a merge folds from registers
 
 // Merges of the sequences queued in `list` (rows of sequence, first slot, parts), all at once.
 // An item is 8 consecutive output dims of one head of one queued sequence; each thread takes
-// one item per round.  A wave loads only as many segments as the longest sequence among its
-// items has (a wave-uniform bound, so the loads need no divergent branch), and every load is
-// issued before any fold, so the queue costs about one memory latency per blockDim.x items.
-// Sequences with more than kMergeRegs segments are merged afterwards from global memory.
+// one item per round.  Segments are folded in groups of kMergeRegs: a group's loads are all
+// issued before its fold, and a wave loads only as many segments of a group as the longest
+// sequence among its items has (a wave-uniform bound, so the loads need no divergent branch).
+// So a round costs one memory latency per group; sequences of up to kMergeRegs parts (the
+// usual case) take one group, and their result is the plain fold of all parts at once.
 template <typename T, int D>
 struct MergeItem {
   float2 ml[kMergeRegs];
   float4 po[kMergeRegs][2];
+  float mu = 0.f, den = 0.f;  // running reference max (0 while no part is seen) and weight sum
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int b = -1, h = 0, d = 0, nseg = 0;
-  // Item `item` of `nitems` (>= 1): which sequence, head and dims, and its segment count
-  // (capped at kMergeRegs).  Items past the end repeat the last one and are not stored.
+  // Item `item` of `nitems` (>= 1): which sequence, head and dims, and its segment count.
+  // Items past the end repeat the last one and are not stored.
   __device__ __forceinline__ int locate(const int (*list)[3], int per, int item, int nitems) {
     const bool real = item < nitems;
     const int it = real ? item : nitems - 1;
     const int i = it / per, r = it - i * per;
     nseg = list[i][2];
-    b = (real && nseg <= kMergeRegs) ? list[i][0] : -1;  // longer ones are merged from global memory
+    b = real ? list[i][0] : -1;
     h = r / (D / 8);
     d = (r - h * (D / 8)) * 8;
     return i;
   }
-  // Loads of segments 0 .. nsw - 1 (nsw wave-uniform, >= this item's capped segment count),
-  // from clamped indices.
-  __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int i, int nsw) {
-    const int ns = nseg < kMergeRegs ? nseg : kMergeRegs;
+  // Loads of segments g0 .. g0 + nsw - 1 (nsw wave-uniform, 1 .. kMergeRegs), from indices
+  // clamped into this item's segments.
+  __device__ __forceinline__ void load(const DecodeParams& P, const int (*list)[3], int i, int g0, int nsw) {
     const int64_t slot0 = list[i][1];
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
       if (s < nsw) {
-        const int64_t slot = slot0 + (s < ns ? s : ns - 1);
+        const int64_t slot = slot0 + (g0 + s < nseg ? g0 + s : nseg - 1);
         ml[s] = P.part_ml[slot * P.ml_stride + h];
         const float4* src = reinterpret_cast<const float4*>(P.part_o + (slot * P.hq + h) * D + d);
         po[s][0] = src[0];
         po[s][1] = src[1];
-      } else {  // (never selected by finish: set so that no value is left undefined)
+      } else {  // (never folded: set so that no value is left undefined)
         ml[s] = make_float2(-INFINITY, 0.f);
         po[s][0] = po[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
   }
-  // Fold of the first nsw (wave-uniform, >= this item's capped segment count) loaded segments.
-  // The fold is vector-ALU work repeated by every thread of the merging workgroup, so it runs
-  // only over the wave's own segment count and uses v_exp_f32 (arguments <= 0) directly.
-  __device__ __forceinline__ void finish(const DecodeParams& P, int nsw) const {
-    if (b < 0) return;
+  // Fold of the loaded segments g0 .. g0 + nsw - 1 that this item has.  The fold is vector-ALU
+  // work repeated by every thread of the merging workgroup, so it runs only over the wave's own
+  // segment count and uses v_exp_f32 (arguments <= 0) directly.
+  __device__ __forceinline__ void fold(int g0, int nsw) {
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
       if (s >= nsw) break;
-      M = s < nseg ? fmaxf(M, ml[s].x) : M;
+      M = g0 + s < nseg ? fmaxf(M, ml[s].x) : M;
     }
-    const float mu = M == -INFINITY ? 0.f : M;
-    float den = 0.f;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (g0 > 0) {  // rescale what the earlier groups folded to the new reference max
+      const float mn = M > mu || den == 0.f ? M : mu;
+      const float m2 = mn == -INFINITY ? 0.f : mn;
+      const float f = den > 0.f ? __builtin_amdgcn_exp2f(mu - m2) : 0.f;
+      den *= f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] *= f;
+      mu = m2;
+    } else {
+      mu = M == -INFINITY ? 0.f : M;
+    }
 #pragma unroll
     for (int s = 0; s < kMergeRegs; ++s) {
       if (s >= nsw) break;
-      const float c = (s < nseg && ml[s].y > 0.f) ? __builtin_amdgcn_exp2f(ml[s].x - mu) * ml[s].y : 0.f;
+      const float c = (g0 + s < nseg && ml[s].y > 0.f) ? __builtin_amdgcn_exp2f(ml[s].x - mu) * ml[s].y : 0.f;
       den += c;
       // Partial rows are finite (normalised averages of finite value rows; a segment whose
       // tokens were all masked stores zeros), and loads past this item's segment count repeat a
@@ -205,6 +214,9 @@ struct MergeItem {
 #pragma unroll
       for (int x = 0; x < 8; ++x) acc[x] = __builtin_fmaf(c, v[x], acc[x]);
     }
+  }
+  __device__ __forceinline__ void store(const DecodeParams& P) const {
+    if (b < 0) return;
     const float inv = den > 0.f ? 1.f / den : 0.f;
     T* orow = reinterpret_cast<T*>(P.out) + b * P.o_sn + h * P.o_sh + d;
     if (sizeof(T) == 2 && P.o_vec) {
@@ -222,9 +234,6 @@ struct MergeItem {
 };
 
 template <typename T, int D>
-__device__ __forceinline__ void merge_partials(const DecodeParams& P, int b, int slot_lo, int nseg);
-
-template <typename T, int D>
 __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*list)[3], int nm) {
   const int per = P.hq * (D / 8);
   const int nitems = nm * per;
@@ -232,13 +241,21 @@ __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*
   auto round = [&](int base) __attribute__((always_inline)) {
     MergeItem<T, D> a;
     const int i = a.locate(list, per, base + threadIdx.x, nitems);
-    int nsw = a.nseg < kMergeRegs ? a.nseg : kMergeRegs;  // the wave's longest item
+    int nsmax = a.nseg;  // the wave's longest item
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) nsw = max(nsw, __shfl_xor(nsw, off, 64));
-    nsw = __builtin_amdgcn_readfirstlane(nsw);
-    a.load(P, list, i, nsw);
-    asm volatile("" ::: "memory");  // every load is issued before the fold
-    a.finish(P, nsw);
+    for (int off = 32; off > 0; off >>= 1) nsmax = max(nsmax, __shfl_xor(nsmax, off, 64));
+    nsmax = __builtin_amdgcn_readfirstlane(nsmax);
+    int nsw = nsmax < kMergeRegs ? nsmax : kMergeRegs;
+    a.load(P, list, i, 0, nsw);
+    asm volatile("" ::: "memory");  // every load of the group is issued before the fold
+    a.fold(0, nsw);
+    for (int g0 = kMergeRegs; g0 < nsmax; g0 += kMergeRegs) {
+      nsw = nsmax - g0 < kMergeRegs ? nsmax - g0 : kMergeRegs;
+      a.load(P, list, i, g0, nsw);
+      asm volatile("" ::: "memory");
+      a.fold(g0, nsw);
+    }
+    a.store(P);
   };
   // The first round (all of it when nitems <= blockDim.x, the usual case) is peeled off the
   // loop: inside a loop, registers that the previous round's loads filled can make the
@@ -248,8 +265,6 @@ __device__ __forceinline__ void merge_queued(const DecodeParams& P, const int (*
   if (nitems <= 0) return;
   round(0);
   for (int base = nt; base < nitems; base += nt) round(base);
-  for (int i = 0; i < nm; ++i)
-    if (list[i][2] > kMergeRegs) merge_partials<T, D>(P, list[i][0], list[i][1], list[i][2]);
 }
 
 // Merge of sequence b's partials (slots slot_lo .. slot_lo + nseg - 1) straight from global
