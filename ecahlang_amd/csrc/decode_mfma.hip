@@ -756,6 +756,18 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         const uint4 a = *reinterpret_cast<const uint4*>(krow + (((4 * s + lg) ^ kx<RB>(lr)) << 4));
         sacc = Mma<T>::qk(a, qop[s], sacc);
       }
+      // the K operand reads run up to four ahead of their (chained) products; left to itself the
+      // compiler reuses one operand register and waits out each read's LDS latency in turn
+      {
+        constexpr int AH = KS < 4 ? KS : 4;
+        __builtin_amdgcn_sched_group_barrier(0x100, AH, 0);  // DS reads
+#pragma unroll
+        for (int x = 0; x < KS - AH; ++x) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, AH, 0);
+      }
       // next page: fixed (rank j takes j, j+J, ...: reproducible) or, with PKV_DECODE_DYNAMIC,
       // the head block's next page on demand (waves finish together; the summation order varies)
       int nxt = pi + J;
@@ -815,13 +827,28 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
           const uint2 p0 = hn == 2 * u ? pb : make_uint2(0, 0);
           const uint2 p1 = hn == 2 * u + 1 ? pb : make_uint2(0, 0);
           const uint4 pp = make_uint4(p0.x, p0.y, p1.x, p1.y);
+          // the V^T operand reads run two output tiles ahead of their products (the same
+          // register reuse as for K otherwise serialises them)
+          uint2 va[MT], vb[MT];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const int c0 = ((2 * u) * D) / 8 + 2 * mt + ((lr & 3) >> 1);
             const int c1 = c0 + D / 8;
-            const uint2 va = lds_read_tr16(trb + ((c0 ^ vx<RB>(tr_row)) << 4));
-            const uint2 vb = lds_read_tr16(trb + ((c1 ^ vx<RB>(tr_row)) << 4));
-            o[mt] = Mma<T>::qk(make_uint4(va.x, va.y, vb.x, vb.y), pp, o[mt]);
+            va[mt] = lds_read_tr16(trb + ((c0 ^ vx<RB>(tr_row)) << 4));
+            vb[mt] = lds_read_tr16(trb + ((c1 ^ vx<RB>(tr_row)) << 4));
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            o[mt] = Mma<T>::qk(make_uint4(va[mt].x, va[mt].y, vb[mt].x, vb[mt].y), pp, o[mt]);
+          {
+            constexpr int AH = MT < 2 ? MT : 2;
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * AH, 0);
+#pragma unroll
+            for (int x = 0; x < MT - AH; ++x) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, AH, 0);
           }
         }
       }
