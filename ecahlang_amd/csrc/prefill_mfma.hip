@@ -511,9 +511,10 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
 }
 
 // Folds the partials of each split group: group = {first_slot, nslots, qo_start, t0, tq, h}.
-// A workgroup takes kMergeRows rows of one group; D/4 lanes per row, 4 dims each.  Loads are
-// issued kMergeUnroll slots at a time from clamped (always valid) addresses, so that they are
-// in flight together.
+// A workgroup takes kMergeRows rows of one group; D/4 lanes per row, 4 dims each.  Each round
+// loads kMergeUnroll slots' (max, sum) and rows together, from clamped (always valid)
+// addresses, and folds them under a running max: one memory round trip per round, and for a
+// group of at most kMergeUnroll slots the plain fold under the group's max.
 constexpr int kMergeUnroll = 4;
 template <int D>
 constexpr int merge_rows() { return 256 / (D / 4); }
@@ -529,13 +530,6 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P,
   const float2* ml = P.part_ml + (int64_t)s0 * kRows + r;
   const int64_t po = ((int64_t)s0 * kRows + r) * D + d;  // element offset of slot s0's dims
   float M = -INFINITY;
-  for (int s = 0; s < ns; s += kMergeUnroll) {
-    float2 v[kMergeUnroll];
-#pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) v[u] = ml[(int64_t)min(s + u, ns - 1) * kRows];
-#pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) M = fmaxf(M, v[u].x);
-  }
   float den = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s = 0; s < ns; s += kMergeUnroll) {
@@ -553,6 +547,20 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P,
       } else {
         v[u] = *reinterpret_cast<const float4*>(P.part_o + po + sl * kRows * D);
       }
+    }
+    // the running max over the slots loaded so far (repeats of the last slot included, as in a
+    // separate max pass); what earlier rounds folded is rescaled to it
+    float Mn = M;
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) Mn = fmaxf(Mn, w[u].x);
+    if (Mn > M) {
+      const float f = den > 0.f ? exp2f(M - Mn) : 0.f;
+      den *= f;
+      acc.x *= f;
+      acc.y *= f;
+      acc.z *= f;
+      acc.w *= f;
+      M = Mn;
     }
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
