@@ -858,7 +858,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the paged-KV path is sharded by sequence across GPUs with no exchange; "
-              "multi-GPU runs are out of scope for this build)", file=sys.stderr)
+              "multi-GPU runs are not measured here)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -210,7 +210,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each XCD a
   // run of consecutive ranges keeps a split sequence's partials mostly on one L2.
   const int w0 = (N0 % 8 == 0) ? (int)(blockIdx.x % 8) * (N0 / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
-  // The first range's head (round 1), its segment records and its first 256 page ids are
+  // The first range's head (fetch 1), its segment records and its first 256 page ids are
   // requested before anything else: none depends on another, and the set-up code below (several
   // hundred instructions) then runs while they are in flight.
   int hv0 = 0, pv0 = 0;
@@ -496,8 +496,8 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     const int32_t* rec = P.sched + (int64_t)w * kRecStride;
     const int32_t* head = P.sched_head + (int64_t)w * kHeadWords;
     lds_barrier();  // the previous range's readers of s_pid / s_seg / the query rows are done
-    // ---- round 1: the range's head: header and first segments (words 0..63), first 64 page ids
-    // (the first range's were requested at the start, with its first two round-2 jobs)
+    // ---- fetch 1: the range's head: header and first segments (words 0..63), first 64 page ids
+    // (the first range's were requested at the start, with its first two fetch-2 jobs)
     const bool first = early && w == w0;
     const int hv = first ? hv0 : head[lane];
     const int pv = first ? pv0 : head[kHeadPidOff + lane];
@@ -507,9 +507,9 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     len = len < 0 ? 0 : (len > kRangePages ? kRangePages : len);
     int nseg = __builtin_amdgcn_readlane(hv, kHdrNseg);
     nseg = nseg < 0 ? 0 : (nseg > len ? len : nseg);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // round 1 complete (compiler-visible vmcnt(0))
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // fetch 1 complete (compiler-visible vmcnt(0))
     if (w >= rmax) break;
-    // the early copies into s_seg / s_pid stand for this range's first two round-2 jobs, unless a
+    // the early copies into s_seg / s_pid stand for this range's first two fetch-2 jobs, unless a
     // prefix item carried by the range has since reused those arrays
     bool early_jobs = first;
     if constexpr (CASC) {
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       }
     }
     if (nseg == 0) continue;
-    // segment s < kHeadSegs from the round-1 registers
+    // segment s < kHeadSegs from the fetch-1 registers
     auto seg_reg = [&](int s) __attribute__((always_inline)) -> int4 {
       return make_int4(__builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s),
                        __builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s + 1),
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
                        __builtin_amdgcn_readlane(hv, kRecSegOff + 4 * s + 3));
     };
     const int qs = min(nseg, qcap);
-    // ---- round 2 (copies into LDS): segment records, page ids, query rows of the first qs
+    // ---- fetch 2 (copies into LDS): segment records, page ids, query rows of the first qs
     // segments, then this wave's first unit.  Job k of the first three kinds is wave k % W's.
     const int npj = (len + 255) / 256;
     const int qchunks = qs * (qrow / 16);

@@ -1,5 +1,5 @@
 """bench.py's command-line contract on the CPU: more than one GPU is refused with a message
-(this build measures one GPU), and every workload name is accepted by the parser."""
+(bench.py measures one GPU), and every workload name is accepted by the parser."""
 import subprocess
 import sys
 from pathlib import Path
