@@ -511,41 +511,46 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(PrefillMfmaParams P) 
 }
 
 // Folds the partials of each split group: group = {first_slot, nslots, qo_start, t0, tq, h}.
-// A workgroup takes kMergeRows rows of one group; D/4 lanes per row, 4 dims each.  Each round
-// loads kMergeUnroll slots' (max, sum) and rows together, from clamped (always valid)
-// addresses, and folds them under a running max: one memory round trip per round, and for a
-// group of at most kMergeUnroll slots the plain fold under the group's max.
+// A workgroup takes merge_rows() rows of one group; D/8 lanes per row, 8 dims each (16-byte
+// loads of fp16 partials).  Each round loads kMergeUnroll slots' (max, sum) and rows together,
+// from clamped (always valid) addresses, and folds them under a running max: one memory round
+// trip per round, and for a group of at most kMergeUnroll slots the plain fold under the
+// group's max.
 constexpr int kMergeUnroll = 4;
 template <int D>
-constexpr int merge_rows() { return 256 / (D / 4); }
+constexpr int merge_rows() { return 256 / (D / 8); }
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P, const int32_t* groups) {
-  constexpr int RB = merge_rows<D>(), TPR = D / 4;
+  constexpr int RB = merge_rows<D>(), TPR = D / 8;
   const int32_t* gr = groups + (int64_t)kGroup * (blockIdx.x / (kRows / RB));
   const int s0 = gr[0], ns = gr[1], qo_start = gr[2], t0 = gr[3], tq = gr[4], h = gr[5];
-  const int r = (blockIdx.x % (kRows / RB)) * RB + threadIdx.x / TPR, d = (threadIdx.x % TPR) * 4;
+  const int r = (blockIdx.x % (kRows / RB)) * RB + threadIdx.x / TPR, d = (threadIdx.x % TPR) * 8;
   const int tt = r / G, hh = r % G;
   if (tt >= tq || ns <= 0) return;
   const float2* ml = P.part_ml + (int64_t)s0 * kRows + r;
   const int64_t po = ((int64_t)s0 * kRows + r) * D + d;  // element offset of slot s0's dims
   float M = -INFINITY;
   float den = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < ns; s += kMergeUnroll) {
     float2 w[kMergeUnroll];
-    float4 v[kMergeUnroll];
+    float v[kMergeUnroll][8];
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
       const int64_t sl = min(s + u, ns - 1);
       w[u] = ml[sl * kRows];
       if constexpr (kHalfPartials<T>) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(reinterpret_cast<const _Float16*>(P.part_o) + po + sl * kRows * D);
-        _Float16 hv[4];
-        __builtin_memcpy(hv, &raw, 8);
-        v[u] = make_float4((float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]);
+        const uint4 raw = *reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(P.part_o) + po + sl * kRows * D);
+        _Float16 hv[8];
+        __builtin_memcpy(hv, &raw, 16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[u][e] = (float)hv[e];
       } else {
-        v[u] = *reinterpret_cast<const float4*>(P.part_o + po + sl * kRows * D);
+        const float4* src = reinterpret_cast<const float4*>(P.part_o + po + sl * kRows * D);
+        const float4 a = src[0], b = src[1];
+        v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
+        v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
       }
     }
     // the running max over the slots loaded so far (repeats of the last slot included, as in a
@@ -556,10 +561,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P,
     if (Mn > M) {
       const float f = den > 0.f ? exp2f(M - Mn) : 0.f;
       den *= f;
-      acc.x *= f;
-      acc.y *= f;
-      acc.z *= f;
-      acc.w *= f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= f;
       M = Mn;
     }
 #pragma unroll
@@ -569,24 +572,23 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMfmaParams P,
       const float c = (s + u < ns && w[u].y > 0.f) ? exp2f(w[u].x - M) * w[u].y : 0.f;
       if (c != 0.f) {
         den += c;
-        acc.x += c * v[u].x;
-        acc.y += c * v[u].y;
-        acc.z += c * v[u].z;
-        acc.w += c * v[u].w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += c * v[u][e];
       }
     }
   }
   const float inv = den > 0.f ? 1.f / den : 0.f;
   T* orow = reinterpret_cast<T*>(P.out) + (int64_t)(qo_start + t0 + tt) * P.o_sn + (int64_t)(h * G + hh) * P.o_sh + d;
   if (P.o_vec) {
-    T v[4] = {from_f32<T>(acc.x * inv), from_f32<T>(acc.y * inv), from_f32<T>(acc.z * inv),
-              from_f32<T>(acc.w * inv)};
-    *reinterpret_cast<uint2*>(orow) = *reinterpret_cast<const uint2*>(v);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      T o4[4] = {from_f32<T>(acc[4 * half] * inv), from_f32<T>(acc[4 * half + 1] * inv),
+                 from_f32<T>(acc[4 * half + 2] * inv), from_f32<T>(acc[4 * half + 3] * inv)};
+      *reinterpret_cast<uint2*>(orow + 4 * half) = *reinterpret_cast<const uint2*>(o4);
+    }
   } else {
-    orow[0] = from_f32<T>(acc.x * inv);
-    orow[1] = from_f32<T>(acc.y * inv);
-    orow[2] = from_f32<T>(acc.z * inv);
-    orow[3] = from_f32<T>(acc.w * inv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) orow[e] = from_f32<T>(acc[e] * inv);
   }
 }
 
