@@ -656,8 +656,32 @@ __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logi
   uint32_t ts = 1;
   int cts = count_ge(1);
   if (cts > 2 * k) {  // (uniform) bisect: count(lo) >= k > count(hi)
-    uint32_t lo = 1, hi = mk + 1u;
-    while (hi - lo > 1u) {
+    // first by value, between the slice's smallest and largest logits (for a smooth spread of
+    // logits this reaches the k..2k band in fewer steps than halving the key range), then by key
+    uint32_t mn_inv = 0;
+#pragma unroll
+    for (int i = 0; i < kSliceTiles * 8; ++i) mn_inv = max(mn_inv, key[i] ? ~key[i] : 0u);
+    mn_inv = block_max_u256(mn_inv, redk);
+    uint32_t lo = ~mn_inv, hi = mk + 1u;  // count(lo) = cts (every non-NaN logit)
+    bool done = false;
+    for (int it = 0; it < 8 && hi - lo > 1u; ++it) {
+      const float fl = key_float(lo), fh = key_float(hi - 1u);
+      if (!(fabsf(fl) <= 3.4e38f) || !(fabsf(fh) <= 3.4e38f)) break;  // non-finite ends: by key
+      const uint32_t mid = fkey(fl + 0.5f * (fh - fl));
+      if (mid <= lo || mid >= hi) break;
+      const int c = count_ge(mid);
+      if (c >= k) {
+        lo = mid;
+        cts = c;
+        if (c <= 2 * k) {
+          done = true;
+          break;
+        }
+      } else {
+        hi = mid;
+      }
+    }
+    while (!done && hi - lo > 1u) {
       const uint32_t mid = lo + ((hi - lo) >> 1);
       const int c = count_ge(mid);
       if (c >= k) {
