@@ -772,7 +772,9 @@ def cpu_baseline(wb, reps=5):
     }
 
 
-def parity(wb, out_dev):
+def parity(wb, out_dev, cache_dev=None):
+    """The decode output against the float64 oracle on the oracle's appended cache; with
+    cache_dev, that cache bit for bit against the device's after its append."""
     import numpy as np
     import torch
     from oracle import kv_ref
@@ -787,7 +789,10 @@ def parity(wb, out_dev):
     got = out_dev.float().cpu().numpy()
     err = np.abs(got - ref)
     ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
-    return {"max_abs_err": float(err.max()), "within_atol2e-3_rtol1e-2": ok}
+    res = {"max_abs_err": float(err.max()), "within_atol2e-3_rtol1e-2": ok}
+    if cache_dev is not None:
+        res["append_bitexact"] = bool(np.array_equal(cache_dev.view(iv).cpu().numpy(), raw))
+    return res
 
 
 def extras(args, torch, runs):
@@ -917,12 +922,22 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
     def decode_valu(l):
         wv.run(dv.q, kv[l], out=outs[l], force_valu=True)
 
-    # eager warm-up and parity on layer 0
+    def decode_append(l):  # the step's append fused into the decode launch
+        w.run(dv.q, kv[l], out=outs[l], append_kv=(dv.k_new, dv.v_new))
+
+    # eager warm-up; parity of the timed step's launch (the append fused into the decode) on
+    # layer 0: the output against the oracle, the appended cache bit for bit, and the plain
+    # decode of the appended cache bitwise equal to the fused output
+    decode_append(0)
+    fused_out = outs[0].clone()
     for l in range(NL):
         append(l)
         decode(l)
     torch.cuda.synchronize()
-    par = None if args.no_check else parity(wb, outs[0])
+    par = None
+    if not args.no_check:
+        par = parity(wb, fused_out, kv[0])
+        par["fused_equals_plain"] = bool(torch.equal(fused_out.view(torch.int16), outs[0].view(torch.int16)))
     print(f"bench: parity {par}", file=sys.stderr, flush=True)
 
     if args.profile_launches:
@@ -949,9 +964,6 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
             with torch.cuda.graph(g, stream=stream):
                 fn()
         return g
-
-    def decode_append(l):  # the step's append fused into the decode launch
-        w.run(dv.q, kv[l], out=outs[l], append_kv=(dv.k_new, dv.v_new))
 
     step_graphs = [capture(lambda l=l: decode_append(l)) for l in range(NL)]
     REP = 8  # launches per layer inside the per-kernel timing graphs

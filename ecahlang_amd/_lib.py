@@ -38,6 +38,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "pkv_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i64]),
     "pkv_decode_workspace_init": (_i32, [_vp, _i32, _vp]),
+    "pkv_decode_schedule_layout": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _vp]),
     "pkv_decode_plan": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
     "pkv_decode_uses_mfma": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "pkv_batch_decode": (

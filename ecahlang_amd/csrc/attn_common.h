@@ -53,6 +53,27 @@ struct DecodeParams {
   int64_t ak_sn, ak_sh, av_sn, av_sh;
 };
 
+// The kernel arguments as wave-uniform values that the compiler cannot reload from the argument
+// block.  Kernel arguments are invariant, so under scalar-register pressure the compiler re-issues
+// their scalar loads instead of keeping them, and a reload that misses the scalar cache costs
+// ~0.25 us per line (measured on MI355X) -- several of those sat in every range's fold and merge.
+// Staged through LDS (one word per thread) and read back with readfirstlane, each field is an
+// ordinary value: kept in scalar registers or spilled to vector lanes, never reloaded.  All
+// threads of the workgroup must call it (it synchronises once).
+template <typename Prm>
+__device__ __forceinline__ Prm uniform_params(const Prm& arg, int* lds_words) {
+  static_assert(sizeof(Prm) % 4 == 0 && sizeof(Prm) / 4 <= 256, "parameter block");
+  constexpr int N = sizeof(Prm) / 4;
+  if ((int)threadIdx.x < N) lds_words[threadIdx.x] = reinterpret_cast<const int*>(&arg)[threadIdx.x];
+  __syncthreads();
+  int w[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_readfirstlane(lds_words[k]);
+  Prm out;
+  __builtin_memcpy(&out, w, sizeof(Prm));
+  return out;
+}
+
 // A part_ml slot (one segment's (max, sum) pairs of every q head) spans whole 128-byte L2 lines,
 // so no line holds two slots.  The merger of a sequence reads its slots with plain loads; were a
 // line shared with another sequence's slot, that load could bring the other slot's line into
@@ -136,6 +157,58 @@ __device__ __forceinline__ void lds_barrier() {
 
 constexpr int kMergeRegs = 8;  // segments a merge folds from registers
 
+// Running merge of a sequence's normalised partial rows: part s holds NV values po[s][.] of the
+// normalised row and its (max, sum) ml[s] in base-2 units.  Parts are folded in groups of
+// kMergeRegs with a running reference max.  Every merge of decode partials uses this one
+// sequence of operations, so an output row does not depend on which workgroup merged it or how
+// (from memory after the last arrival, or straight from the last part's own state).
+template <int NV>
+struct MergeAcc {
+  float mu = 0.f, den = 0.f;  // running reference max (0 while no part is seen) and weight sum
+  float acc[NV];
+  __device__ __forceinline__ MergeAcc() {
+#pragma unroll
+    for (int x = 0; x < NV; ++x) acc[x] = 0.f;
+  }
+  // Fold of parts g0 .. g0 + nsw - 1 (the group's values in ml[0 .. nsw), po[0 .. nsw)), those
+  // below nseg only.  v_exp_f32 directly: its arguments are <= 0.
+  __device__ __forceinline__ void fold(const float2* ml, const float (*po)[NV], int g0, int nsw, int nseg) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s >= nsw) break;
+      M = g0 + s < nseg ? fmaxf(M, ml[s].x) : M;
+    }
+    if (g0 > 0) {  // rescale what the earlier groups folded to the new reference max
+      const float mn = M > mu || den == 0.f ? M : mu;
+      const float m2 = mn == -INFINITY ? 0.f : mn;
+      const float f = den > 0.f ? __builtin_amdgcn_exp2f(mu - m2) : 0.f;
+      den *= f;
+#pragma unroll
+      for (int x = 0; x < NV; ++x) acc[x] *= f;
+      mu = m2;
+    } else {
+      mu = M == -INFINITY ? 0.f : M;
+    }
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s >= nsw) break;
+      const float c = (g0 + s < nseg && ml[s].y > 0.f) ? __builtin_amdgcn_exp2f(ml[s].x - mu) * ml[s].y : 0.f;
+      den += c;
+      // Partial rows are finite (normalised averages of finite value rows; a segment whose
+      // tokens were all masked stores zeros), and entries past nseg repeat a real part, so
+      // c * row needs no select.
+#pragma unroll
+      for (int x = 0; x < NV; ++x) acc[x] = __builtin_fmaf(c, po[s][x], acc[x]);
+    }
+  }
+  // Output value x (a sum of exact zeros comes out +0, whatever the signs of its terms).
+  __device__ __forceinline__ float out(int x) const {
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    return (acc[x] + 0.f) * inv;
+  }
+};
+
 // Merges of the sequences queued in `list` (rows of sequence, first slot, parts), all at once.
 // An item is 8 consecutive output dims of one head of one queued sequence; each thread takes
 // one item per round.  Segments are folded in groups of kMergeRegs: a group's loads are all
@@ -146,9 +219,8 @@ constexpr int kMergeRegs = 8;  // segments a merge folds from registers
 template <typename T, int D>
 struct MergeItem {
   float2 ml[kMergeRegs];
-  float4 po[kMergeRegs][2];
-  float mu = 0.f, den = 0.f;  // running reference max (0 while no part is seen) and weight sum
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float po[kMergeRegs][8];
+  MergeAcc<8> m;
   int b = -1, h = 0, d = 0, nseg = 0;
   // Item `item` of `nitems` (>= 1): which sequence, head and dims, and its segment count.
   // Items past the end repeat the last one and are not stored.
@@ -172,63 +244,30 @@ struct MergeItem {
         const int64_t slot = slot0 + (g0 + s < nseg ? g0 + s : nseg - 1);
         ml[s] = P.part_ml[slot * P.ml_stride + h];
         const float4* src = reinterpret_cast<const float4*>(P.part_o + (slot * P.hq + h) * D + d);
-        po[s][0] = src[0];
-        po[s][1] = src[1];
+        const float4 a = src[0], c = src[1];
+        po[s][0] = a.x; po[s][1] = a.y; po[s][2] = a.z; po[s][3] = a.w;
+        po[s][4] = c.x; po[s][5] = c.y; po[s][6] = c.z; po[s][7] = c.w;
       } else {  // (never folded: set so that no value is left undefined)
         ml[s] = make_float2(-INFINITY, 0.f);
-        po[s][0] = po[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) po[s][x] = 0.f;
       }
     }
   }
-  // Fold of the loaded segments g0 .. g0 + nsw - 1 that this item has.  The fold is vector-ALU
-  // work repeated by every thread of the merging workgroup, so it runs only over the wave's own
-  // segment count and uses v_exp_f32 (arguments <= 0) directly.
-  __device__ __forceinline__ void fold(int g0, int nsw) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < kMergeRegs; ++s) {
-      if (s >= nsw) break;
-      M = g0 + s < nseg ? fmaxf(M, ml[s].x) : M;
-    }
-    if (g0 > 0) {  // rescale what the earlier groups folded to the new reference max
-      const float mn = M > mu || den == 0.f ? M : mu;
-      const float m2 = mn == -INFINITY ? 0.f : mn;
-      const float f = den > 0.f ? __builtin_amdgcn_exp2f(mu - m2) : 0.f;
-      den *= f;
-#pragma unroll
-      for (int x = 0; x < 8; ++x) acc[x] *= f;
-      mu = m2;
-    } else {
-      mu = M == -INFINITY ? 0.f : M;
-    }
-#pragma unroll
-    for (int s = 0; s < kMergeRegs; ++s) {
-      if (s >= nsw) break;
-      const float c = (g0 + s < nseg && ml[s].y > 0.f) ? __builtin_amdgcn_exp2f(ml[s].x - mu) * ml[s].y : 0.f;
-      den += c;
-      // Partial rows are finite (normalised averages of finite value rows; a segment whose
-      // tokens were all masked stores zeros), and loads past this item's segment count repeat a
-      // real segment, so c * row needs no select.
-      const float v[8] = {po[s][0].x, po[s][0].y, po[s][0].z, po[s][0].w,
-                          po[s][1].x, po[s][1].y, po[s][1].z, po[s][1].w};
-#pragma unroll
-      for (int x = 0; x < 8; ++x) acc[x] = __builtin_fmaf(c, v[x], acc[x]);
-    }
-  }
+  __device__ __forceinline__ void fold(int g0, int nsw) { m.fold(ml, po, g0, nsw, nseg); }
   __device__ __forceinline__ void store(const DecodeParams& P) const {
     if (b < 0) return;
-    const float inv = den > 0.f ? 1.f / den : 0.f;
     T* orow = reinterpret_cast<T*>(P.out) + b * P.o_sn + h * P.o_sh + d;
     if (sizeof(T) == 2 && P.o_vec) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        T v[4] = {from_f32<T>(acc[4 * half] * inv), from_f32<T>(acc[4 * half + 1] * inv),
-                  from_f32<T>(acc[4 * half + 2] * inv), from_f32<T>(acc[4 * half + 3] * inv)};
+        T v[4] = {from_f32<T>(m.out(4 * half)), from_f32<T>(m.out(4 * half + 1)),
+                  from_f32<T>(m.out(4 * half + 2)), from_f32<T>(m.out(4 * half + 3))};
         *reinterpret_cast<uint2*>(orow + 4 * half) = *reinterpret_cast<const uint2*>(v);
       }
     } else {
 #pragma unroll
-      for (int x = 0; x < 8; ++x) orow[x] = from_f32<T>(acc[x] * inv);
+      for (int x = 0; x < 8; ++x) orow[x] = from_f32<T>(m.out(x));
     }
   }
 };

@@ -102,6 +102,23 @@ extern "C" int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_head
   return (int64_t)ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices).total;
 }
 
+extern "C" int pkv_decode_schedule_layout(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
+                                          int32_t num_ctas, int64_t num_indices, int64_t workspace_bytes,
+                                          int64_t* out) {
+  if (!out || !ws_args_ok(batch, num_qo_heads, head_dim, num_ctas, num_indices)) return kBadArg;
+  const WsLayout L = ws_layout(batch, num_qo_heads, head_dim, num_ctas, num_indices, workspace_bytes);
+  if ((int64_t)L.total > workspace_bytes) return kWorkspaceTooSmall;
+  out[0] = (int64_t)L.ghdr;
+  out[1] = (int64_t)L.heads;
+  out[2] = (int64_t)L.recs;
+  out[3] = (int64_t)L.precs;
+  out[4] = L.rcap;
+  out[5] = L.slots;
+  out[6] = kHeadWords;
+  out[7] = kRecStride;
+  return kOk;
+}
+
 extern "C" int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream) {
   if (batch <= 0) return kOk;
   // A fill kernel rather than a memset node, so the call is also safe under graph capture.

@@ -26,9 +26,7 @@
 // the current K is consumed, its V as soon as the current V is.  At a segment (sequence) end the
 // J states meet in LDS; the owner of each 16-dim tile writes it: output rows, or the partial of a
 // sequence split across ranges, merged by the last workgroup to finish (attn_common.h).
-#include "attn_common.h"
-#include "mfma_common.h"
-#include "decode_sched.h"
+#include "decode_tile.h"
 #include "../../include/pagedkv.h"
 
 using namespace pkv;
@@ -36,48 +34,11 @@ using namespace pkv;
 namespace {
 
 using namespace pkv::mfma;
+using namespace pkv::dtile;
 
-constexpr int W = 8;                // waves per workgroup
-constexpr int NT = W * 64;
 constexpr int kQArea = 8192;        // LDS bytes for query rows of the range's first segments
 constexpr int kSegLds = 64;         // segment records staged in LDS (more are read from memory)
 constexpr int kMaxSplit = 64;       // split segments whose arrival a workgroup defers
-constexpr float kLazyMax = 8.f;     // a column's reference max moves only on jumps > 2^8
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-// One wave-wide copy global -> LDS: lane l's 16 bytes at src (per lane) land at LDS byte
-// dst + 16 l (dst wave-uniform, in M0).  Inline assembly, so the compiler neither tracks nor
-// waits for it: the kernel orders these copies with explicit vmcnt waits.  `nt` streams the
-// K/V pages past the caches; small metadata copies use the default policy.
-__device__ __forceinline__ void dma16_nt(const void* src, const char* dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0) : "memory");
-}
-__device__ __forceinline__ void dma16(const void* src, const char* dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)(dst));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
-}
-
-// XOR swizzles of 16-byte chunk positions inside a staged row of RB bytes (the low four bits
-// only, so a row's chunks stay in their own 256-byte half and every copy still reads whole
-// lines).  K rows are read as the QK A operand (16 rows, one chunk per 16-lane group): distinct
-// bank groups for the 16 rows.  V rows are read by ds_read_b64_tr_b16 (per 32 lanes, 8 rows x 2
-// adjacent chunks): distinct bank groups for those 16 chunks.
-template <int RB>
-__device__ __forceinline__ int kx(int t) {
-  return RB >= 256 ? (t & 15) : ((t >> 1) & 7);
-}
-template <int RB>
-__device__ __forceinline__ int vx(int t) {
-  return RB >= 256 ? 2 * (t & 7) : 2 * ((t >> 1) & 3);
-}
 
 // Sum of the J (<= W) copies of a tile, read four at a time with every read of a batch issued
 // before any add (copies past J repeat copy 0 and are dropped).
@@ -96,49 +57,8 @@ __device__ __forceinline__ f4 fold_copies(int J, F&& copy) {
   return acc;
 }
 
-struct Seg {
-  int b, beg, end, nv, slot0, part, nparts, np;
-  int app_page, app_row;  // range page and row of the step's new token (-1: not in this segment)
-};
-// A segment word (decode_sched.h), clamped so that a stale or malformed schedule cannot index
-// past the batch, the record or the partial slots.
-__device__ __forceinline__ Seg unpack_seg(int4 v, int len, int batch, int slot_cap) {
-  Seg s;
-  const int b = v.x & ((1 << kSegBBits) - 1);
-  s.b = b >= batch ? batch - 1 : b;
-  const int nv = (int)(((unsigned)v.x >> kSegBBits) & 31);
-  s.nv = nv > 16 ? 16 : nv;
-  s.np = (int)((unsigned)v.x >> (kSegBBits + 5));
-  s.beg = v.y & 0x3FF;
-  s.end = (v.y >> 16) & 0xFFFF;
-  s.end = s.end > len ? len : s.end;
-  s.beg = s.beg > s.end ? s.end : s.beg;
-  const int app = (v.y >> 10) & 63;
-  s.app_page = app ? s.end - 1 - ((app - 1) >> 4) : -1;
-  s.app_page = s.app_page >= s.beg ? s.app_page : -1;
-  s.app_row = (app - 1) & 15;
-  s.nparts = ((v.w >> 16) & 0xFFFF) + 1;
-  s.nparts = s.nparts > slot_cap ? slot_cap : s.nparts;
-  s.slot0 = v.z < 0 ? 0 : (v.z > slot_cap - s.nparts ? slot_cap - s.nparts : v.z);
-  s.part = v.w & 0xFFFF;
-  s.part = s.part >= s.nparts ? s.nparts - 1 : s.part;
-  s.np = s.np >= s.nparts ? s.nparts - 1 : s.np;
-  return s;
-}
-
 template <int HB, int D>
-struct Shape {
-  static constexpr int RW = HB * D;        // elements of a unit row
-  static constexpr int RB = RW * 2;        // bytes of a unit row
-  static constexpr int CPR = RB / 16;      // 16-byte chunks per row
-  static constexpr int RPI = 64 / CPR;     // rows per 1 KB copy
-  static constexpr int NI = 16 / RPI;      // copies per K (or V) tile
-  static constexpr int TILE = 16 * RB;     // bytes of a K (or V) tile
-  static constexpr int KS = RW / 32;       // QK steps
-  static constexpr int KSH = D / 32;       // QK steps per head
-  static constexpr int MT = D / 16;        // output tiles of 16 dims
-  static constexpr int LDS = W * 2 * TILE + kQArea;  // dynamic LDS
-};
+constexpr int mfma_lds_bytes() { return W * 2 * Shape<HB, D>::TILE + kQArea; }
 
 // CASC: the schedule may hold prefix items (a cascade plan).  Without it the prefix-item code is
 // not compiled in, which keeps the range loop's registers free of its pressure.
@@ -202,9 +122,6 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   auto page_ok = [&](int pid) __attribute__((always_inline)) -> bool {
     return pid >= 0 && (int64_t)pid < P.num_pages;
   };
-  // a range record's page id word: the page, and whether other sequences read it too
-  auto pid_page = [](int raw) __attribute__((always_inline)) -> int { return raw < 0 ? raw : raw & ~kPidShared; };
-  auto pid_cached = [](int raw) __attribute__((always_inline)) -> bool { return raw >= 0 && (raw & kPidShared); };
 
   const int N0 = P.num_ctas;
   // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each XCD a
@@ -578,11 +495,11 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     auto seg_at = [&](int s) __attribute__((always_inline)) -> Seg {
       int4 v;
       if (s < kSegLds) {
-        v = s_seg[s];
+        v = lds_ld<int4>(s_seg + s);
         v = make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                       __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
       } else {
-        v = *reinterpret_cast<const int4*>(rec + kRecSegOff + 4 * s);
+        v = glb_ld16_sync<int4>(rec + kRecSegOff + 4 * s);
         v = make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                       __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
       }
@@ -603,8 +520,9 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
           const int c = lane % (2 * CPR), cc = c % CPR;
           const bool isv = c >= CPR;
           const int64_t h = (int64_t)hb * HB + cc / (D / 8);
-          const char* src = isv ? P.av + (int64_t)sg.b * P.av_sn + h * P.av_sh
-                                : P.ak + (int64_t)sg.b * P.ak_sn + h * P.ak_sh;
+          const int64_t kb = uniform64((int64_t)(P.ak + (int64_t)sg.b * P.ak_sn)), ksh = uniform64(P.ak_sh);
+          const int64_t vb = uniform64((int64_t)(P.av + (int64_t)sg.b * P.av_sn)), vsh = uniform64(P.av_sh);
+          const char* src = (const char*)((isv ? vb : kb) + h * (isv ? vsh : ksh));
           dma16(src + 16 * (cc % (D / 8)), reinterpret_cast<const char*>(&s_x[0][wave][0]));
         }
       }
@@ -613,11 +531,12 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       if (si < qs) {
         const char* src = qarea + si * qrow + qh * D * 2 + 16 * lg;
 #pragma unroll
-        for (int s = 0; s < KSH; ++s) qv[s] = *reinterpret_cast<const uint4*>(src + 64 * s);
+        for (int s = 0; s < KSH; ++s) qv[s] = lds_ld<uint4>(src + 64 * s);
+        asm volatile("" ::: "memory");
       } else {
         const T* src = qall + (int64_t)sg.b * P.q_sn + (int64_t)qh * P.q_sh + 8 * lg;
 #pragma unroll
-        for (int s = 0; s < KSH; ++s) qv[s] = *reinterpret_cast<const uint4*>(src + 32 * s);
+        for (int s = 0; s < KSH; ++s) qv[s] = glb_ld16_sync<uint4>(src + 32 * s);
       }
 #pragma unroll
       for (int s = 0; s < KS; ++s) qop[s] = (colv && hn == s / KSH) ? qv[s % KSH] : make_uint4(0, 0, 0, 0);
@@ -873,16 +792,9 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   }
 }
 
-// Head block: the largest power of two HB with HB * g <= 16, HB * D <= 256 and HB | Hkv.
-int head_block(int d, int g, int hkv) {
-  int hb = 1;
-  while (2 * hb * g <= 16 && 2 * hb * d <= 256 && hkv % (2 * hb) == 0) hb *= 2;
-  return hb;
-}
-
 template <typename T, int D, int HB>
 int launch(const DecodeParams& P, hipStream_t s) {
-  constexpr int lds = Shape<HB, D>::LDS;
+  constexpr int lds = mfma_lds_bytes<HB, D>();
   if (P.cascade)
     hipLaunchKernelGGL((decode_mfma_kernel<T, D, HB, true>), dim3(P.num_ctas), dim3(NT), lds, s, P);
   else
@@ -892,7 +804,7 @@ int launch(const DecodeParams& P, hipStream_t s) {
 
 template <typename T>
 int launch_t(const DecodeParams& P, int d, hipStream_t s) {
-  const int hb = head_block(d, P.hq / P.hkv, P.hkv);
+  const int hb = decode_head_block(d, P.hq / P.hkv, P.hkv);
   if (d == 128) return hb == 2 ? launch<T, 128, 2>(P, s) : launch<T, 128, 1>(P, s);
   return hb == 4 ? launch<T, 64, 4>(P, s) : (hb == 2 ? launch<T, 64, 2>(P, s) : launch<T, 64, 1>(P, s));
 }
@@ -905,7 +817,7 @@ bool decode_mfma_supported(int dtype, int d, int g, int hkv, int batch) {
   (void)batch;
   if (!((dtype == kF16 || dtype == kBF16) && (d == 64 || d == 128) && g >= 1 && g <= 16 && hkv >= 1))
     return false;
-  return hkv / head_block(d, g, hkv) <= W;
+  return hkv / decode_head_block(d, g, hkv) <= W;
 }
 
 // Sequences that share one prefix item, G = W * NB * (16 / g) (NB = 2 blocks per wave, 1 when
@@ -919,6 +831,7 @@ int decode_mfma_group(int d, int g, int hkv) {
 
 int decode_mfma_dispatch(const DecodeParams& P, int dtype, int d, hipStream_t s) {
   if (P.ps != 16) return decode_valu_dispatch(P, dtype, d, s);
+  // plain schedules with the fixed page order: each wave streams one run of its range's pages
   return dtype == kF16 ? launch_t<_Float16>(P, d, s) : launch_t<__hip_bfloat16>(P, d, s);
 }
 

@@ -87,6 +87,14 @@ constexpr int kMaxPrefixNp = 31;                       // chunks per prefix at m
 // reads (one head's rows of C pages) times kPrefixCostNum / kPrefixCostDen.
 constexpr int kPrefixCostNum = 1, kPrefixCostDen = 1;
 
+// Head block of the matrix-core decode: the largest power of two HB with HB * g <= 16 query heads
+// (the MFMA's 16 columns), HB * head_dim <= 256 and HB | Hkv.
+__host__ __device__ inline int decode_head_block(int d, int g, int hkv) {
+  int hb = 1;
+  while (2 * hb * g <= 16 && 2 * hb * d <= 256 && hkv % (2 * hb) == 0) hb *= 2;
+  return hb;
+}
+
 // Segment word packing.
 constexpr int kSegBBits = 22;
 __host__ __device__ inline int seg_pack_range(int beg, int end, int app) { return beg | (app << 10) | (end << 16); }

@@ -55,6 +55,9 @@ __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* t
     else ok = ok && col < stride && pos >= 1 && pos <= stack_size && pairs && n < pairs_cap;
     if (!ok) {
       if (threadIdx.x == 0 && err) atomicAdd(err, 1);
+      // a rejected copy on write still owns its pair: mark it empty, so the data copy skips it
+      // rather than replaying an earlier call's pair onto a page that may have changed hands
+      if (threadIdx.x == 0 && kind == 3 && pairs && n >= 0 && n < pairs_cap) pairs[2 * n] = pairs[2 * n + 1] = -1;
     } else if (kind == 3) {
       if (threadIdx.x == 0) {
         int32_t* cell = table + (int64_t)row * stride + col;
@@ -78,11 +81,13 @@ __global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* t
 // The data of copy-on-write pairs: for pair p and layer l (blockIdx.y, blockIdx.z), the page
 // pairs[2p] of the layer is copied to the page pairs[2p + 1], 16 bytes per thread (the page is
 // whole 16-byte runs: 2 x page_size x Hkv x head_dim elements).  Pairs naming a page outside
-// the pool are skipped and counted in *err.
+// the pool are skipped and counted in *err; a (-1, -1) pair (a rejected copy on write, counted
+// when it was rejected) is skipped silently.
 __global__ void pool_copy_pages_kernel(char* cache, int64_t layer_stride, int64_t page_bytes, const int32_t* pairs,
                                        int64_t num_pages, int32_t* err) {
   const int p = blockIdx.y, l = blockIdx.z;
   const int src = pairs[2 * p], dst = pairs[2 * p + 1];
+  if (src == -1 && dst == -1) return;  // a rejected copy on write (already counted)
   if (src < 0 || src >= num_pages || dst < 0 || dst >= num_pages) {
     if (err && l == 0 && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(err, 1);
     return;

@@ -116,12 +116,31 @@ def llama32_1b_decode(seed=1001) -> PagedBatch:
                        pool_pages=256, scale=1.0)
 
 
+def qwen25_3b_lengths(seed=1002, batch=64, lo=512, hi=4096) -> list:
+    """Tokens per sequence after the step's append: context U[lo, hi] + 1."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    return [c + 1 for c in torch.randint(lo, hi + 1, (batch,), generator=g).tolist()]
+
+
 def qwen25_3b_decode(seed=1002, batch=64, lo=512, hi=4096) -> PagedBatch:
     """16 q / 2 kv heads, head_dim 128, fp16; context U[lo, hi]; pool 1.25x the pages used."""
-    g = torch.Generator().manual_seed(seed + 7919)
-    ctx = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
-    return build_batch([c + 1 for c in ctx], [1] * batch, 16, 2, 128, torch.float16, seed,
+    return build_batch(qwen25_3b_lengths(seed, batch, lo, hi), [1] * batch, 16, 2, 128, torch.float16, seed,
                        scale=0.5)
+
+
+def paged_table(kv_len, pool_pages, seed, ps=16):
+    """(indptr, indices, last) int32 host tensors: each sequence's pages a run of a seeded random
+    permutation of the pool (the page table device_decode_batch builds for the same arguments)."""
+    gen = torch.Generator().manual_seed(seed)
+    npages = [(int(L) + ps - 1) // ps for L in kv_len]
+    total = sum(npages)
+    if pool_pages < total:
+        raise ValueError("pool smaller than the pages the batch needs")
+    indices = torch.randperm(pool_pages, generator=gen)[:total].to(torch.int32)
+    indptr = torch.zeros(len(kv_len) + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(npages, dtype=torch.int64), 0).to(torch.int32)
+    last = torch.tensor([((int(L) - 1) % ps) + 1 if L else 0 for L in kv_len], dtype=torch.int32)
+    return indptr, indices, last
 
 
 def qwen25_3b_prefill(seed=1003, requests=8, chunk=512, max_prefix=8192) -> PagedBatch:
@@ -169,16 +188,9 @@ def device_decode_batch(kv_len, hq, hkv, d, dtype, seed, pool_pages, device, *, 
     """Pages of each sequence scattered by a seeded permutation of the pool (host); the used
     pages filled with N(0,1)*scale on the device, every other slot (unused pages and the
     slots past each sequence's last token) NaN."""
-    gen = torch.Generator().manual_seed(seed)
     kv_len = [int(x) for x in kv_len]
-    npages = [(L + ps - 1) // ps for L in kv_len]
-    total = sum(npages)
-    if pool_pages < total:
-        raise ValueError("pool smaller than the pages the batch needs")
-    indices = torch.randperm(pool_pages, generator=gen)[:total].to(torch.int32)
-    indptr = torch.zeros(len(kv_len) + 1, dtype=torch.int32)
-    indptr[1:] = torch.cumsum(torch.tensor(npages, dtype=torch.int64), 0).to(torch.int32)
-    last = torch.tensor([((L - 1) % ps) + 1 if L > 0 else 0 for L in kv_len], dtype=torch.int32)
+    indptr, indices, last = paged_table(kv_len, pool_pages, seed, ps)
+    total = int(indptr[-1])
     dgen = torch.Generator(device=device).manual_seed(seed)
     cache = torch.full((pool_pages, 2, ps, hkv, d), float("nan"), dtype=dtype, device=device)
     idx = indices.to(device).long()
@@ -196,15 +208,23 @@ def device_decode_batch(kv_len, hq, hkv, d, dtype, seed, pool_pages, device, *, 
                              indices.to(device), last.to(device), q)
 
 
+def llama31_8b_lengths(seed=1004, batch=128, lo=1024, hi=32768) -> list:
+    """Tokens per sequence after the step's append: context log-uniform in [lo, hi] + 1."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    u = torch.rand(batch, generator=g, dtype=torch.float64)
+    ctx = torch.floor(torch.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))).long().tolist()
+    return [c + 1 for c in ctx]
+
+
+LLAMA31_8B_POOL_PAGES = 20_000_000_000 // (2 * 16 * 8 * 128 * 2)  # a ~20 GB pool of 64 KiB pages
+
+
 def llama31_8b_decode_device(device, seed=1004, batch=128, lo=1024, hi=32768,
                              pool_bytes=20_000_000_000) -> DeviceDecodeBatch:
     """Long-context decode at Llama-3.1-8B shape (32 q / 8 kv heads, head_dim 128, bf16):
     context log-uniform in [lo, hi], pages scattered over a pool of ~pool_bytes."""
-    g = torch.Generator().manual_seed(seed + 7919)
-    u = torch.rand(batch, generator=g, dtype=torch.float64)
-    ctx = torch.floor(torch.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))).long().tolist()
     page_bytes = 2 * 16 * 8 * 128 * 2
-    return device_decode_batch([c + 1 for c in ctx], 32, 8, 128, torch.bfloat16, seed,
+    return device_decode_batch(llama31_8b_lengths(seed, batch, lo, hi), 32, 8, 128, torch.bfloat16, seed,
                                pool_bytes // page_bytes, device)
 
 

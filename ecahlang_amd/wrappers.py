@@ -70,6 +70,12 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._use_cuda_graph = use_cuda_graph
         self._planned = False
         self._counters_ready = 0  # batch size whose counters are known to be zero
+        # Whether this wrapper's schedules carry cascade prefix items.  run() picks the kernel
+        # variant from it when it is enqueued, so a run captured in a graph keeps the variant of
+        # its plan: once a run has been captured, a plan that changes it is refused (replays
+        # would run the wrong variant on the new schedule).
+        self._cascade_mode = False
+        self._captured_mode: bool | None = None
 
     @property
     def is_cuda_graph_enabled(self) -> bool:
@@ -78,6 +84,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
     def reset_workspace_buffer(self, float_workspace_buffer: torch.Tensor, *_args) -> None:
         self._workspace = float_workspace_buffer
         self._counters_ready = 0
+        self._captured_mode = None
 
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
              num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
@@ -144,6 +151,12 @@ class BatchDecodeWithPagedKVCacheWrapper:
             if self._shared.numel() < self._batch:
                 raise ValueError("kv_shared_pages must have one entry per sequence")
             shared = self._shared.data_ptr()
+        cascade = bool(cascade) and kv_shared_pages is not None
+        if self._captured_mode is not None and cascade != self._captured_mode:
+            raise ValueError("plan(cascade=...) must not change after a run of this wrapper was captured "
+                             "in a graph (replays keep the kernel variant of the captured plan); "
+                             "use another wrapper or reset_workspace_buffer()")
+        self._cascade_mode = cascade
         if self._mfma:
             # the matrix-core kernel's schedule, built on the device from this page table
             check(lib().pkv_decode_plan(self._indptr.data_ptr(), self._indices.data_ptr(),
@@ -165,6 +178,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
         ecahlang/manager.py:270-280) -- in the same launch on the matrix-core path."""
         if not self._planned:
             raise RuntimeError("plan() must be called before run()")
+        if torch.cuda.is_current_stream_capturing():
+            self._captured_mode = self._cascade_mode
         if return_lse or lse is not None:
             raise NotImplementedError("return_lse is not implemented")
         if q_scale is not None or k_scale is not None or v_scale is not None:

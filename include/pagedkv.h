@@ -111,6 +111,16 @@ int pkv_append_paged_kv_cache_rope(const void* q, int64_t q_stride_n, int64_t q_
 int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
                                    int32_t num_ctas, int64_t num_indices);
 
+/* Where pkv_decode_plan puts its schedule inside a workspace of workspace_bytes for this geometry.
+ * A host-only diagnostic for tests and tools that read the schedule back; no counterpart in the
+ * reference.  out[0..7] = byte offsets of the global header, the range heads and the range
+ * records and the prefix item records, then the range capacity, the partial slot capacity, the
+ * words per range head and the words per range record (record formats: decode_sched.h).
+ * Returns 0, or PKV_E_ARG / PKV_E_WORKSPACE as pkv_decode_plan would. */
+int pkv_decode_schedule_layout(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
+                               int32_t num_ctas, int64_t num_indices, int64_t workspace_bytes,
+                               int64_t* out);
+
 /* Zeroes the split-merge counters at the head of the workspace (the device half of plan).
  * pkv_batch_decode leaves them zero again when it finishes, so this is needed only when the
  * buffer is fresh or the batch grows. */

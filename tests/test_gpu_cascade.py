@@ -9,6 +9,8 @@ import numpy as np
 import pytest
 import torch
 
+import sched_check as sc
+
 from ecahlang_amd.wrappers import BatchDecodeWithPagedKVCacheWrapper
 from oracle import kv_ref
 
@@ -59,7 +61,7 @@ def _decode(dv, hq, hkv, d, dtype, hint, cascade=False):
     out = w.run(dv["q"], dv["cache"])
     torch.cuda.synchronize()
     # global schedule header (after the per-sequence counters, 256-byte aligned): R, prefix items
-    off = (4 * dv["q"].shape[0] + 255) // 256 * 256
+    off = sc.layout(dv["q"].shape[0], hq, d, w._ctas, dv["indices"].numel(), ws.numel())["ghdr"]
     hdr = ws[off:off + 32].view(torch.int32).tolist()
     return out.float().cpu().numpy(), hdr[0], hdr[4]
 

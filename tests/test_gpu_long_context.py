@@ -1,9 +1,9 @@
 """Long-context decode at full size: Llama-3.1-8B shape (32 q / 8 kv heads, head_dim 128,
 bf16), batch 128, contexts log-uniform in [1024, 32768] (~73k pages, ~4.8 GB of K/V) scattered
 over a ~20 GB pool.  Every sequence is split across many workgroups.  The matrix-core output is
-checked against the vector-ALU kernel for all sequences, and against the float64 oracle for 33
-sequences at evenly spaced length ranks, from the shortest (inside one or two ranges) to the
-longest (split over the most ranges), their K/V read back from the device."""
+checked against the float64 oracle for every sequence, its K/V read back from the device, and
+against the vector-ALU kernel (tests/test_gpu_decode_exact.py checks the same shape's outputs in
+closed form, which a dropped or repeated page cannot pass)."""
 import numpy as np
 import pytest
 import torch
@@ -36,11 +36,8 @@ def test_llama31_8b_long_context_decode_full_size():
     np.testing.assert_allclose(o.cpu().numpy(), ov.cpu().numpy(), atol=4e-3, rtol=2e-2)
 
     lens = np.array(wb.kv_len)
-    order = np.argsort(lens, kind="stable")
-    pick = sorted({int(order[i]) for i in np.linspace(0, B - 1, 33).round().astype(int)})
-    assert len(pick) == 33
     indptr = wb.indptr.cpu().numpy()
-    for b in pick:
+    for b in range(B):
         pages = wb.indices[indptr[b]:indptr[b + 1]].long()
         L = int(lens[b])
         k = wb.cache[pages, 0].reshape(-1, wb.hkv, wb.d)[:L].float().cpu().numpy()

@@ -7,6 +7,8 @@ import numpy as np
 import pytest
 import torch
 
+import sched_check as sc
+
 from ecahlang_amd import workloads
 from oracle import kv_ref
 from oracle.manager_ref import RefKVCacheManager
@@ -133,7 +135,7 @@ def test_full_size_cascade_and_hint_match_plain():
         torch.cuda.synchronize()
         outs[mode] = out.float()
         # the plan's global header (after the per-sequence words): [ranges, ..., prefix items]
-        off = (4 * B + 255) // 256 * 256
+        off = sc.layout(B, loop.hq, loop.d, w._ctas, m._cg_kv_indices[B].numel(), w._workspace.numel())["ghdr"]
         items[mode] = w._workspace[off:off + 32].view(torch.int32).tolist()[4]
     assert items["plain"] == 0 and items["cascade"] > 0, items
     assert torch.isfinite(outs["cascade"]).all()
