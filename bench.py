@@ -410,6 +410,8 @@ def bulk_append(args, torch, workloads, ops, dev):
         wb = workloads.build_batch([p + 512 for p in prefix], [512] * requests, 16, 2, 128, torch.float16,
                                    seed=4100 + requests, fill_old=False)
         nnz = wb.k_new.shape[0]
+        if requests == 128:
+            host_big = wb
         print(f"bench: bulk append, nnz {nnz}", file=sys.stderr, flush=True)
         dv = wb.to(dev)
 
@@ -465,15 +467,25 @@ def bulk_append(args, torch, workloads, ops, dev):
                         parity_bitexact=ok)
         del dv
     big = res[max(res)]
-    # CPU baseline: the oracle append (numpy scatter) of 4096 tokens, median of 3
-    sb = workloads.build_batch([512] * 8, [512] * 8, 16, 2, 128, torch.float16, seed=3, fill_old=False)
-    iv = lambda t: t.view(torch.int16).numpy()
+    # CPU baseline: the same 65,536-token append on the host cores with torch's index_put (the
+    # page and slot of each token from the page table, then one scatter of the K rows and one of
+    # the V rows into the pool), median of 3
+    ncores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(ncores)
+    cpool = host_big.cache.clone()
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        kv_ref.append(iv(sb.cache), iv(sb.k_new), iv(sb.v_new), sb.batch_indices.numpy(), sb.positions.numpy(),
-                      sb.indices.numpy(), sb.indptr.numpy(), 16)
+        pos, bi = host_big.positions.long(), host_big.batch_indices.long()
+        page = host_big.indices.long()[host_big.indptr.long()[bi] + pos // 16]
+        slot = pos % 16
+        cpool[page, 0, slot] = host_big.k_new
+        cpool[page, 1, slot] = host_big.v_new
         times.append(time.perf_counter() - t0)
+    cores_used = torch.get_num_threads()
+    torch.set_num_threads(prev_threads)
+    del cpool
     result = {
         "metric": "paged K/V append GB/s (% HBM peak), Qwen2.5-3B, 65536 tokens",
         "value": big["gbs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "fp16",
@@ -484,9 +496,10 @@ def bulk_append(args, torch, workloads, ops, dev):
         "by_nnz": {str(k): v for k, v in sorted(res.items())},
         "roofline": {"bound": "hbm", "achieved": big["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": big["frac"], "traffic": traffic},
-        "cpu_baseline": {"value": round(append_bytes(sb) / statistics.median(times) / 1e9, 3), "unit": "GB/s",
-                         "cores": 1, "kind": "port",
-                         "sample": "4096 tokens: the oracle append (numpy scatter, which also copies its pool), median of 3",
+        "cpu_baseline": {"value": round(append_bytes(host_big) / statistics.median(times) / 1e9, 3), "unit": "GB/s",
+                         "cores": cores_used, "kind": "port",
+                         "sample": "the 65,536-token append itself: torch index_put of the K and V rows on the host "
+                                   "cores, median of 3",
                          "cpu_model": cpu_model()},
     }
     return result

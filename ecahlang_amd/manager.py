@@ -67,10 +67,12 @@ class _Staging:
     """Host -> device copies of int32 arrays through a ring of reused pinned buffers, queued on
     the current stream.  ``host(n)`` hands out the next buffer once the event recorded behind
     its last copy has completed (so a queued copy never sees its source change); ``send`` queues
-    the copy and records the buffer's event.  Arrays beyond the ring's capacity, and copies made
-    while the stream is being captured, go through a fresh pinned buffer instead, which the
-    caching host allocator keeps until its copy has run; a copy recorded into a graph reads its
-    buffer at every replay, so those buffers are kept for the life of the staging ring."""
+    the copy and records the buffer's event.  Arrays beyond the ring's capacity go through a
+    fresh pinned buffer instead, which the caching host allocator keeps until its copy has run.
+    Nothing is staged while the stream is being captured: a pinned allocation is not allowed
+    then, and a recorded copy would read its buffer again at every replay, so ``host`` raises
+    before anything is enqueued (the callers fill their metadata before capture, as the
+    reference's loop does, or use the device-resident steps)."""
 
     def __init__(self, device: torch.device, slots: int = 8, cap: int = 1 << 15):
         self.device, self.cap = device, cap
@@ -79,11 +81,14 @@ class _Staging:
         self.events = [torch.cuda.Event() for _ in range(slots)]
         self.used = [False] * slots
         self.i = 0
-        self.captured: list = []  # pinned sources of copies recorded into graphs
 
     def host(self, n: int) -> tuple:
         """(slot, int32 array of n to fill); slot -1 means the array is not a ring buffer."""
-        if n > self.cap or torch.cuda.is_current_stream_capturing():
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("page-pool metadata is staged from host arrays and cannot be recorded into a "
+                               "graph: fill it before capture (fill_cuda_graph_metadata) or capture the "
+                               "device-resident step (begin_device_steps / device_step)")
+        if n > self.cap:
             return -1, np.empty(n, dtype=np.int32)
         i = self.i
         self.i = (i + 1) % len(self.bufs)
@@ -96,8 +101,6 @@ class _Staging:
         ``dst`` is None."""
         n = len(arr)
         src = self.bufs[slot][:n] if slot >= 0 else torch.from_numpy(arr).pin_memory()
-        if slot < 0 and torch.cuda.is_current_stream_capturing():
-            self.captured.append(src)
         if dst is None:
             dst = torch.empty(n, dtype=torch.int32, device=self.device)
         dst[:n].copy_(src, non_blocking=True)

@@ -393,3 +393,30 @@ def test_default_pool_sizing_from_free_device_memory():
     assert list(m.allocate("a", 40)) == [m.max_blocks - 1, m.max_blocks - 2, m.max_blocks - 3]
     m.free("a")
     assert m.pool_errors() == 0
+
+
+def test_metadata_staging_refuses_graph_capture():
+    """Staging host arrays cannot be recorded into a graph (no pinned allocation during capture,
+    and a recorded copy would re-read its buffer at every replay): the call raises before
+    anything is enqueued, and the pool is unchanged and usable afterwards."""
+    m = _pool(64, stride=8)
+    m.allocate(0, 40)
+    m.allocate(1, 20)
+    want = [t.clone() for t in m.get_append_metadata([0, 1])]
+    m.allocate(2, 33)  # a queued pop, flushed by the next staging call
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="cannot be recorded into a graph"):
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                m.get_append_metadata([0, 1])
+    got = m.get_append_metadata([0, 1])
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+    ref = RefKVCacheManager(m.max_blocks)
+    for i, n in ((0, 40), (1, 20), (2, 33)):
+        ref.allocate(i, n)
+    assert m.batch_to_blocks[2] == ref.batch_to_blocks[2]
+    assert list(m.free_blocks) == ref.free_blocks
+    assert m.pool_errors() == 0

@@ -53,3 +53,26 @@ def test_noalloc_decode_matches_workspace_decode_twice(case):
         ref = kv_ref.decode(wb.q.float().numpy(), vals, wb.indptr.numpy(), wb.indices.numpy(), wb.last.numpy(),
                             wb.ps)
         np.testing.assert_allclose(got.float().cpu().numpy(), ref, atol=2e-3, rtol=1e-2)
+
+
+def test_noalloc_vector_alu_path_matches_workspace_decode_twice():
+    """fp32 takes the vector-ALU decode (no plan): the array's split counters and partials
+    against a caller workspace, bitwise, on two calls in a row, the second smaller."""
+    for i, (lens, seed) in enumerate([([37, 900, 1500, 16, 333, 1200, 64, 700, 2048, 5, 480, 1001], 21),
+                                      ([300, 17, 90], 22)]):
+        wb = workloads.build_batch(lens, [1] * len(lens), 8, 2, 64, torch.float32, seed=seed)
+        print(f"fp32 call {i}: B={wb.batch} pages={int(wb.indptr[-1])}", flush=True)
+        dv = wb.to(DEV)
+        ops.append_paged_kv_cache(dv.k_new, dv.v_new, dv.batch_indices, dv.positions, dv.cache, dv.indices,
+                                  dv.indptr, dv.last)
+        ctas = 64
+        w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=DEV))
+        w.plan(dv.indptr, dv.indices, dv.last, wb.hq, wb.hkv, wb.d, wb.ps, q_data_type=wb.dtype, num_ctas=ctas)
+        assert not w._mfma
+        want = w.run(dv.q, dv.cache)
+        got = _noalloc(dv, ctas)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32)), f"fp32 call {i}"
+        ref = kv_ref.decode(wb.q.numpy(), dv.cache.cpu().numpy(), wb.indptr.numpy(), wb.indices.numpy(),
+                            wb.last.numpy(), wb.ps)
+        np.testing.assert_allclose(got.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
