@@ -514,10 +514,12 @@ def step36(args, torch, workloads, dev):
     advance_device_step (AutoKVCacheManager.begin_device_steps); with --host-steps the
     bookkeeping runs on the host per step, as the reference's loop does, and the graph holds
     the layers only.  The timed region of each step runs from before the host's part to the
-    end of the replay; retiring 8 sequences and writing their successors' tokens (the work of
-    a prefill) happens between timed regions.  graph_ms times the replay alone on alternate
-    steps (their host part done before the first event); graph_back_to_back_ms replays the
-    graph with the host enqueueing ahead."""
+    end of the batch change that follows the replay: 8 sequences retired and 8 new ones
+    allocated on the prefix, and with device steps the new batch handed back to the device
+    (begin_device_steps); writing the new sequences' tokens (the work of their prefill) follows
+    the timed region.  batch_change_ms is that batch change alone.  graph_ms times the replay
+    alone on alternate steps (their host part done before the first event, their batch change
+    after the last); graph_back_to_back_ms replays the graph with the host enqueueing ahead."""
     import numpy as np
     steps, warmup = max(1, min(args.steps, 40)), max(1, min(args.warmup, 4))
     print("bench: building the 36-layer shared-prefix decode loop (B=128)", file=sys.stderr, flush=True)
@@ -536,23 +538,36 @@ def step36(args, torch, workloads, dev):
     # Steps alternate between the timed step (host part, then replay) and the same kind of
     # step with the host part done before the first event (the replay alone: graph_ms), so the
     # two figures are taken on the same mix of batch states; each starts on an idle GPU.
-    times, gtimes, byts, gbyts = [], [], [], []
+    times, gtimes, rtimes, byts, gbyts = [], [], [], [], []
     with loop.on_stream():
         for i in range(2 * steps):
             full = i % 2 == 0
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e2 = torch.cuda.Event(enable_timing=True)
             if not full:
                 loop.begin_step()
+            else:
+                sb = loop.step_bytes(ahead=1)  # (the lengths this step attends)
             loop.stream.synchronize()
             e0.record(loop.stream)
             if full:
                 loop.begin_step()
             loop.replay()
             e1.record(loop.stream)
-            e1.synchronize()
-            (times if full else gtimes).append(e0.elapsed_time(e1) / 1e3)
-            (byts if full else gbyts).append(loop.step_bytes())
-            loop.retire()
+            if full:  # the batch change: 8 sequences freed, 8 allocated on the prefix, the new
+                # batch handed to the device (their tokens, the prefill's work, come after)
+                _, new = loop.retire(write_tokens=False)
+                e2.record(loop.stream)
+                e2.synchronize()
+                times.append(e0.elapsed_time(e2) / 1e3)
+                rtimes.append(e1.elapsed_time(e2) / 1e3)
+                byts.append(sb)
+                loop.write_tokens(new)
+            else:
+                e1.synchronize()
+                gtimes.append(e0.elapsed_time(e1) / 1e3)
+                gbyts.append(loop.step_bytes())
+                loop.retire()
     # parity on the last step's layers 0 and 35, 8 sequences each, before the next step
     par = None
     if not args.no_check:
@@ -606,7 +621,8 @@ def step36(args, torch, workloads, dev):
                                + ", 8 sequences retired per step",
                    "layers": L, "batch": loop.batch, "steps": steps, "warmup": warmup,
                    "pool_pages": loop.mgr.max_blocks, "device_steps": device_steps},
-        "step_ms": round(t_step * 1e3, 4), "graph_ms": round(t_graph * 1e3, 4),
+        "step_ms": round(t_step * 1e3, 4), "batch_change_ms": round(float(np.mean(rtimes)) * 1e3, 4),
+        "graph_ms": round(t_graph * 1e3, 4),
         "graph_back_to_back_ms": round(t_b2b * 1e3, 4),
         "unique_bytes_per_step": int(uniq), "logical_bytes_per_step": int(logical),
         "graph_unique_gbs": round(gbs_graph, 2), "logical_gbs": round(logical / t_step / 1e9, 2),
@@ -819,7 +835,8 @@ def extras(args, torch, runs):
     keep = {
         "qwen25_3b_prefill": ("prefill_us", "prefill_valu_us", "flops"),
         "llama31_8b_b128": ("decode_us", "decode_bytes"),
-        "qwen25_3b_step36": ("step_ms", "graph_ms", "graph_back_to_back_ms", "graph_unique_gbs", "parity"),
+        "qwen25_3b_step36": ("step_ms", "batch_change_ms", "graph_ms", "graph_back_to_back_ms", "graph_unique_gbs",
+                             "parity"),
         "qwen25_3b_bulk_append": ("by_nnz",),
     }
     out = {}

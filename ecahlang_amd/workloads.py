@@ -318,7 +318,8 @@ class SharedPrefixDecodeLoop:
         """Fill sequence sid's pages from first_page on (every layer) with fresh values; the
         slots past its last token stay NaN."""
         m = self.mgr
-        m._flush()
+        if m._ops:  # (queued pool operations land first; device-step mode stays on otherwise)
+            m._flush()
         n = m._npages[sid]
         if n <= first_page:
             return
@@ -329,7 +330,7 @@ class SharedPrefixDecodeLoop:
         if last < self.ps:
             cache[:, pages[-1:], :, last:] = float("nan")
 
-    def _start_sequence(self):
+    def _start_sequence(self, write: bool = True):
         sid = f"s{self._next_id}"
         self._next_id += 1
         lo, hi = self.suffix
@@ -337,8 +338,16 @@ class SharedPrefixDecodeLoop:
         tokens = self.prefix_tokens + n
         self.mgr.allocate(sid, tokens, prefix="prefix")
         self._note(("allocate", sid, tokens, "prefix"))
-        self._write_tokens(sid, self.prefix_tokens // self.ps)  # (its pages after the prefix's full ones)
+        if write:
+            self.write_tokens([sid])
         return sid
+
+    def write_tokens(self, sids) -> None:
+        """Write the tokens of newly started sequences (their pages after the prefix's full
+        ones), as their prefill would leave them."""
+        with torch.cuda.stream(self.stream):
+            for sid in sids:
+                self._write_tokens(sid, self.prefix_tokens // self.ps)
 
     # ---------------------------------------------------------------- one step
     @contextlib.contextmanager
@@ -424,17 +433,24 @@ class SharedPrefixDecodeLoop:
                 raise RuntimeError("the page table moved after the graph was captured")
             self.graph.replay()
 
-    def retire(self) -> list:
-        """Finish ``finish`` random sequences and start new ones in their batch rows."""
+    def retire(self, write_tokens: bool = True) -> list:
+        """Finish ``finish`` random sequences and start new ones in their batch rows: the
+        pool's work of a batch change (frees, allocations on the prefix and, with device steps,
+        handing the new batch to the device).  With ``write_tokens`` the new sequences' tokens
+        are written too (the work of their prefill, not of the decode step); otherwise the
+        caller writes them with ``write_tokens(new)`` before the next step.  Returns the rows
+        and the new sequences."""
         with torch.cuda.stream(self.stream):
             rows = torch.randperm(self.batch, generator=self.gen)[: self.finish].tolist()
+            new = []
             for r in sorted(rows):
                 self.mgr.free(self.ids[r])
                 self._note(("free", self.ids[r]))
-                self.ids[r] = self._start_sequence()
-            if self.device_steps:  # the new batch goes back to the device (outside the step)
+                self.ids[r] = self._start_sequence(write=write_tokens)
+                new.append(self.ids[r])
+            if self.device_steps:  # the new batch goes back to the device
                 self._begin_device()
-        return rows
+        return rows, new
 
     def new_inputs(self) -> None:
         with torch.cuda.stream(self.stream):
@@ -445,12 +461,13 @@ class SharedPrefixDecodeLoop:
     def seq_lens(self) -> list:
         return [self.mgr._seq_len(s) for s in self.ids]
 
-    def step_bytes(self) -> dict:
+    def step_bytes(self, ahead: int = 0) -> dict:
         """Bytes one step's attention reads and writes per layer: ``unique`` counts every
-        distinct valid token once (the shared prefix once), ``logical`` once per sequence."""
+        distinct valid token once (the shared prefix once), ``logical`` once per sequence.
+        ``ahead``: the lengths after that many more steps (1 before a step: the step's own)."""
         es = torch.tensor([], dtype=self.dtype).element_size()
         tok = 2 * self.hkv * self.d * es
-        lens = self.seq_lens()
+        lens = [L + ahead for L in self.seq_lens()]
         io = 2 * self.batch * self.hq * self.d * es + self.batch * tok  # q in, o out, appended K/V
         unique = (self.prefix_tokens + sum(L - self.prefix_tokens for L in lens)) * tok + io
         return {"unique": unique, "logical": sum(lens) * tok + io}

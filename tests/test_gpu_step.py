@@ -93,7 +93,8 @@ def test_small_loop_matches_oracle_every_step(hint, cascade, device_steps):
 def test_full_size_step_qwen_36_layers(device_steps):
     """Qwen2.5-3B attention shape, 36 layers, batch 128, 2048-token shared prefix: three steps
     (the graph captured on the first), then layers 0 and 17 checked on 8 sequences and layer 35
-    on all 128."""
+    on all 128; between steps, 8 sequences retired and replaced, their tokens written after the
+    pool's part of the batch change."""
     loop = workloads.SharedPrefixDecodeLoop(DEV, max_steps=6, record=True, device_steps=device_steps)
     ref = RefKVCacheManager(loop.mgr.max_blocks, seq_lens=loop.mgr.seq_lens)
     done = 0
@@ -110,7 +111,12 @@ def test_full_size_step_qwen_36_layers(device_steps):
             rows = list(range(0, loop.batch, loop.batch // 8))
             for layer in (0, 17, 35):
                 _check_layer(loop, layer, rows if layer < 35 else list(range(loop.batch)), idx, ptr, last)
-        loop.retire()
+        # the batch change as the benchmark times it: the pool's part, then the new sequences'
+        # tokens written (with device steps, after the new batch is on the device)
+        _, new = loop.retire(write_tokens=False)
+        loop.write_tokens(new)
+        if device_steps:
+            assert loop.mgr._dev is not None
     assert loop.mgr.pool_errors() == 0
 
 
