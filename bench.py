@@ -32,7 +32,11 @@ roofline.traffic is the decode kernel's HBM bytes per launch measured with hardw
 scaled by the same counter's reading for a plain copy of known size run in the same
 process); it is read from profiles/decode_traffic.json, where those runs were recorded, and is
 reported only when that record was taken on this workload and on these exact decode kernel
-sources (a SHA-256 over them), null otherwise.
+sources (a SHA-256 over them), null otherwise.  The long-context decode, the 36-layer step and
+the bulk append read their own records (profiles/*_traffic.json) the same way.  A record is
+written from the two counter runs' CSV files by
+`bench.py --workload W --traffic-record FETCH.csv WRITE.csv PROFILE.log`, PROFILE.log being
+the output of the counter run (its profile_launches line).
 """
 from __future__ import annotations
 
@@ -63,10 +67,24 @@ def append_bytes(wb) -> int:
     return nnz * (4 * wb.hkv * wb.d * es + 12)
 
 
-DECODE_SOURCES = ("decode.hip", "decode_mfma.hip", "decode_plan.hip", "decode_sched.h", "attn_common.h",
-                  "mfma_common.h", "common.h")
+DECODE_SOURCES = ("decode.hip", "decode_mfma.hip", "decode_plan.hip", "decode_sched.h", "decode_tile.h",
+                  "attn_common.h", "mfma_common.h", "common.h")
 APPEND_SOURCES = ("append.hip", "common.h")
 APPEND_TRAFFIC_FILE = os.path.join(os.path.dirname(TRAFFIC_FILE), "append_traffic.json")
+LONG_TRAFFIC_FILE = os.path.join(os.path.dirname(TRAFFIC_FILE), "decode_traffic_llama31_8b.json")
+STEP36_TRAFFIC_FILE = os.path.join(os.path.dirname(TRAFFIC_FILE), "step36_traffic.json")
+# per workload: (record file, kernel whose dispatches are counted, its sources, workload text)
+TRAFFIC_RECORDS = {
+    "qwen25_3b_b64": (TRAFFIC_FILE, "decode_mfma_kernel", DECODE_SOURCES,
+                      "qwen2.5-3b paged decode, 1 layer, B=64, fp16 (bench.py default)"),
+    "llama31_8b_b128": (LONG_TRAFFIC_FILE, "decode_mfma_kernel", DECODE_SOURCES,
+                        "llama-3.1-8b long-context paged decode, 1 layer, B=128, bf16"),
+    "qwen25_3b_step36": (STEP36_TRAFFIC_FILE, "decode_mfma_kernel", DECODE_SOURCES,
+                         "qwen2.5-3b 36-layer decode step, B=128, 2048-token shared prefix, fp16: each "
+                         "layer's decode launch (the step's append fused in)"),
+    "qwen25_3b_bulk_append": (APPEND_TRAFFIC_FILE, "append_wave_kernel", APPEND_SOURCES,
+                              "append_paged_kv_cache, 128 requests x 512 tokens (nnz 65536), fp16"),
+}
 
 
 def source_hash(names=DECODE_SOURCES) -> str:
@@ -81,10 +99,6 @@ def source_hash(names=DECODE_SOURCES) -> str:
     return h.hexdigest()
 
 
-def decode_source_hash() -> str:
-    return source_hash(DECODE_SOURCES)
-
-
 def _traffic_record(path):
     try:
         with open(path) as f:
@@ -96,19 +110,79 @@ def _traffic_record(path):
 def measured_traffic(wb, w):
     """HBM bytes per decode launch from the committed counter runs, when they were taken on
     this workload, this workgroup count and these decode sources (None otherwise)."""
-    t = _traffic_record(TRAFFIC_FILE)
-    if (t.get("decode_bytes") != decode_bytes(wb) or t.get("decode_ctas") != w._ctas
-            or t.get("decode_source_sha256") != decode_source_hash()):
-        return None
-    return t.get("traffic_bytes")
+    return recorded_traffic("qwen25_3b_b64", decode_bytes(wb), key={"decode_ctas": w._ctas})
 
 
 def measured_append_traffic(wb):
     """HBM bytes per append launch from the committed counter runs (rocprofv3 FETCH_SIZE and
     WRITE_SIZE over `--workload qwen25_3b_bulk_append --profile-launches N`, scaled by a copy
     of the same byte count), when taken on this token batch and these append sources."""
-    t = _traffic_record(APPEND_TRAFFIC_FILE)
-    if t.get("append_bytes") != append_bytes(wb) or t.get("append_source_sha256") != source_hash(APPEND_SOURCES):
+    return recorded_traffic("qwen25_3b_bulk_append", append_bytes(wb))
+
+
+def record_traffic(workload, fetch_csv, write_csv, profile_log):
+    """Write a workload's traffic record from its two counter runs: the kernel's FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch, averaged over the run's last `kernel_dispatches` dispatches of
+    it, the profiled launches), each scaled by the same counter's reading for the plain copies
+    of `copy_bytes` the run made after them (true bytes / reading).  Returns the record."""
+    import csv
+    path, kernel, sources, text = TRAFFIC_RECORDS[workload]
+
+    with open(profile_log) as f:
+        prof = [json.loads(ln) for ln in f if ln.startswith('{"profile_launches"')][-1]
+
+    def readings(fn, counter):
+        kern, copy = [], []
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != counter:
+                    continue
+                if kernel in r["Kernel_Name"]:
+                    kern.append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+                elif "copyBuffer" in r["Kernel_Name"]:
+                    copy.append(float(r["Counter_Value"]))
+        kern = [v for _, v in sorted(kern)][-prof["kernel_dispatches"]:]
+        return kern, copy
+
+    copy_kib = prof["copy_bytes"] / 1024
+    fk, fc = readings(fetch_csv, "FETCH_SIZE")
+    wk, wc = readings(write_csv, "WRITE_SIZE")
+    fc = [v for v in fc if v > 0.4 * copy_kib]  # (the calibration copies, not small ones)
+    wc = [v for v in wc if v > 0.4 * copy_kib]
+    if not (fk and wk and fc and wc):
+        raise SystemExit(f"no {kernel} or calibration-copy dispatches in the counter files")
+    fs, ws = copy_kib / statistics.mean(fc), copy_kib / statistics.mean(wc)
+    traffic = round((statistics.mean(fk) * fs + statistics.mean(wk) * ws) * 1024)
+    algo = prof["algorithmic_bytes"]
+    rec = {"kernel": kernel, "workload": text, "algorithmic_bytes": algo,
+           "fetch_kib_per_dispatch": round(statistics.mean(fk), 1),
+           "write_kib_per_dispatch": round(statistics.mean(wk), 1), "dispatches": len(fk),
+           "copy_bytes": prof["copy_bytes"], "copy_fetch_kib_per_dispatch": round(statistics.mean(fc), 1),
+           "copy_write_kib_per_dispatch": round(statistics.mean(wc), 1),
+           "fetch_scale": round(fs, 5), "write_scale": round(ws, 5), "traffic_bytes": traffic,
+           "traffic_over_algorithmic": round(traffic / algo, 4),
+           "source_sha256": source_hash(sources)}
+    for k in ("key", "logical_bytes"):
+        if k in prof:
+            rec[k] = prof[k]
+    if "logical_bytes" in prof:
+        rec["traffic_over_logical"] = round(traffic / prof["logical_bytes"], 4)
+    with open(path, "w") as f:
+        json.dump(rec, f, indent=1)
+        f.write("\n")
+    return rec
+
+
+def recorded_traffic(workload, algorithmic_bytes=None, key=None):
+    """HBM bytes per launch from a workload's traffic record, when it was taken on these
+    kernel sources and on this workload (its algorithmic bytes or its key); None otherwise."""
+    path, _, sources, _ = TRAFFIC_RECORDS[workload]
+    t = _traffic_record(path)
+    if t.get("source_sha256") != source_hash(sources):
+        return None
+    if algorithmic_bytes is not None and t.get("algorithmic_bytes") != algorithmic_bytes:
+        return None
+    if key is not None and t.get("key") != key:
         return None
     return t.get("traffic_bytes")
 
@@ -147,6 +221,19 @@ def long_context(args, torch, workloads, Wrapper, dev):
     w.plan(wb.indptr, wb.indices, wb.last, wb.hq, wb.hkv, wb.d, wb.ps, q_data_type=wb.dtype,
            num_ctas=args.ctas, deterministic=not args.dynamic)
     out = torch.empty_like(wb.q)
+    if args.profile_launches:  # counter runs: eager launches, then copies of the same byte count
+        for _ in range(args.profile_launches):
+            w.run(wb.q, wb.cache, out=out)
+        nb = dbytes // 16 * 16
+        src = torch.empty(nb // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.profile_launches):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_launches": args.profile_launches, "kernel_dispatches": args.profile_launches,
+                          "algorithmic_bytes": dbytes, "copy_bytes": nb, "key": {"decode_ctas": w._ctas}}),
+              flush=True)
+        return None
     stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):
         w.run(wb.q, wb.cache, out=out)
@@ -194,7 +281,8 @@ def long_context(args, torch, workloads, Wrapper, dev):
         "decode_us": round(t * 1e6, 3), "decode_bytes": dbytes,
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": recorded_traffic("llama31_8b_b128", dbytes, key={"decode_ctas": w._ctas})},
         "cpu_baseline": {"value": round(sample_bytes / statistics.median(times) / 1e9, 3), "unit": "GB/s",
                          "cores": cores, "kind": "port",
                          "sample": f"4 median-length sequences ({sum(int(lens[b]) for b in sample)} tokens): "
@@ -449,7 +537,8 @@ def bulk_append(args, torch, workloads, ops, dev):
             for _ in range(args.profile_launches):
                 dst.copy_(src)
             torch.cuda.synchronize()
-            print(json.dumps({"profile_launches": args.profile_launches, "append_bytes": append_bytes(wb),
+            print(json.dumps({"profile_launches": args.profile_launches,
+                              "kernel_dispatches": args.profile_launches, "algorithmic_bytes": append_bytes(wb),
                               "copy_bytes": nb}), flush=True)
             return None
         REP = 10
@@ -524,12 +613,36 @@ def step36(args, torch, workloads, dev):
     steps, warmup = max(1, min(args.steps, 40)), max(1, min(args.warmup, 4))
     print("bench: building the 36-layer shared-prefix decode loop (B=128)", file=sys.stderr, flush=True)
     device_steps = not args.host_steps
-    loop = workloads.SharedPrefixDecodeLoop(dev, max_steps=2 * steps + warmup + 2, device_steps=device_steps)
+    n_prof = args.profile_launches
+    loop = workloads.SharedPrefixDecodeLoop(dev, max_steps=(n_prof or 2 * steps) + warmup + 2,
+                                            device_steps=device_steps)
     for _ in range(warmup):
         loop.begin_step()
         loop.replay()
         loop.retire()
     torch.cuda.synchronize()
+    step_key = {"layers": loop.layers, "batch": loop.batch, "prefix_tokens": loop.prefix_tokens,
+                "device_steps": device_steps}
+    if n_prof:  # counter runs: n steps (36 decode launches each), then copies of a layer's unique bytes
+        ub, lb = [], []
+        for _ in range(n_prof):
+            b = loop.step_bytes(ahead=1)
+            ub.append(b["unique"])
+            lb.append(b["logical"])
+            loop.begin_step()
+            loop.replay()
+            loop.retire()
+        unique, logical = int(np.mean(ub)), int(np.mean(lb))
+        nb = unique // 16 * 16
+        src = torch.empty(nb // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(n_prof):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_launches": n_prof, "kernel_dispatches": n_prof * loop.layers,
+                          "algorithmic_bytes": unique, "logical_bytes": logical, "copy_bytes": nb,
+                          "key": step_key}), flush=True)
+        return None
     # a cyclic-garbage pass of the interpreter over everything torch has loaded can stall one
     # step's host bookkeeping by tens of ms; collect once and freeze the survivors first
     import gc
@@ -609,6 +722,8 @@ def step36(args, torch, workloads, dev):
                                            v.float().transpose(0, 1)[None], enable_gqa=True)
         ctimes.append(time.perf_counter() - t0)
     sample_bytes = sum(k.numel() * 2 * 2 for k in ks)
+    per_launch = recorded_traffic("qwen25_3b_step36", key=step_key)
+    step_traffic = None if per_launch is None else per_launch * L
     result = {
         "metric": "36-layer decode step (attention path), unique KV GB/s (% HBM peak), Qwen2.5-3B B=128 shared prefix",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
@@ -627,9 +742,11 @@ def step36(args, torch, workloads, dev):
         "unique_bytes_per_step": int(uniq), "logical_bytes_per_step": int(logical),
         "graph_unique_gbs": round(gbs_graph, 2), "logical_gbs": round(logical / t_step / 1e9, 2),
         "parity": par,
-        # (value and roofline share one denominator: the whole step)
+        # (value and roofline share one denominator: the whole step; traffic is the HBM bytes of
+        # the step's 36 decode launches from the counter record, which the record also states per
+        # launch against a layer's unique and logical bytes)
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": step_traffic},
         "cpu_baseline": {"value": round(sample_bytes / statistics.median(ctimes) / 1e9, 3), "unit": "GB/s",
                          "cores": cores, "kind": "port",
                          "sample": f"layer 0, 4 sequences ({sum(k.shape[0] for k in ks)} tokens): gather + fp32 SDPA, median of 3",
@@ -887,9 +1004,17 @@ def main():
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the other workloads' summary (the line's 'extras')")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
-                    help="for counter runs: N eager decode and append launches, then N plain "
-                         "copies of the decode's byte count (the counters' calibration), then exit")
+                    help="for counter runs: N eager launches of the workload's kernel (the 36-layer "
+                         "step: N steps), then N plain copies of its algorithmic byte count per launch "
+                         "(the counters' calibration), then exit")
+    ap.add_argument("--traffic-record", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PROFILE_LOG"),
+                    help="write the workload's traffic record (profiles/*traffic.json) from the "
+                         "counter_collection CSVs of a FETCH_SIZE and a WRITE_SIZE run of "
+                         "--profile-launches and that run's output, then exit (no GPU needed)")
     args = ap.parse_args()
+    if args.traffic_record:
+        print(json.dumps(record_traffic(args.workload, *args.traffic_record)))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the paged-KV path is sharded by sequence across GPUs with no exchange; "
@@ -982,8 +1107,8 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
         for _ in range(n):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_launches": n, "decode_bytes": decode_bytes(wb), "copy_bytes": nb}),
-              flush=True)
+        print(json.dumps({"profile_launches": n, "kernel_dispatches": n, "algorithmic_bytes": decode_bytes(wb),
+                          "copy_bytes": nb, "key": {"decode_ctas": w._ctas}}), flush=True)
         return None
 
     stream = torch.cuda.Stream(device=dev)
