@@ -39,6 +39,18 @@ returns, in page order, the pages only b held (a tail of its list) and drops the
 the rest.  The oracle restates the same rules; the graph metadata's shared-page hint for the
 decode plan is computed on the device from the page lists.
 
+A second extension, also without a counterpart (the reference frees every page of a finished
+sequence and keeps no index of what pages hold, manager.py:99-120): a token-keyed prefix cache,
+enabled by ``prefix_cache_rows``.  ``free(b, tokens=ids)`` keeps b's full pages in a tree keyed
+by their token ids (one node per page, a path from the root per page-aligned prefix) under a
+count of their own; ``allocate(b, T, tokens=ids)`` starts b with the pages of the longest
+cached prefix of ids (the caller then prefills only the tokens after it); pages only the tree
+holds are evicted, least recently used leaf first, when an allocation or an append is short
+of free pages, or by ``evict``.  The tree lives on the host; each insert's page ids are kept
+on the device in a cache row of the page table (the inserting sequence's row copied there), so
+a match is one device copy from that row.  The oracle (``RefRadixKVCacheManager``) states the
+rules.
+
 The sampling helpers (init_sampling_buffers, fill_sampling_params,
 fill_cuda_graph_sampling_params, ``mask_penalty``) are outside the paged-KV path; they are
 kept, as plain tensor code, so that ``main.py`` finds the attributes it uses.
@@ -56,6 +68,18 @@ from .ops import (append_paged_kv_cache, append_paged_kv_cache_slots, get_batch_
                   get_seq_lens)
 
 _POP, _PUSH, _COPY, _COW = 0, 1, 2, 3
+
+
+class _CacheNode:
+    """A page of the prefix cache: its block_size token ids (its key under its parent), the
+    page's handle, its place on the device (cache row and column) and its last use."""
+    __slots__ = ("key", "handle", "parent", "children", "last", "id", "row", "col")
+
+    def __init__(self, key, handle, parent, nid, col):
+        self.key, self.handle, self.parent, self.id, self.col = key, handle, parent, nid, col
+        self.children: dict = {}
+        self.last = 0
+        self.row = -1
 
 
 def get_total_free_memory(index: int = 0) -> int:
@@ -181,10 +205,12 @@ class AutoKVCacheManager:
                  seq_lens: int = 128, block_size: int = 16, dtype: torch.dtype = torch.float16,
                  layout: str = "NHD", total_gpu_mem_bytes: int | None = None,
                  mem_utilization: float = 0.9, *, device=None, max_pages_per_seq: int = 512,
-                 strict_reference_q1: bool = False):
+                 strict_reference_q1: bool = False, prefix_cache_rows: int = 0):
         """manager.py:14-72.  Extensions (keyword-only): ``device`` (default: the current
         CUDA device), ``max_pages_per_seq`` (initial width of the per-sequence page table; it
-        grows on demand) and ``strict_reference_q1`` (see the module docstring)."""
+        grows on demand), ``strict_reference_q1`` (see the module docstring) and
+        ``prefix_cache_rows`` (0: no prefix cache; otherwise how many inserts the cache keeps
+        at once, each in a row of the page table)."""
         if layout.upper() != "NHD":
             raise NotImplementedError("only the NHD cache layout is implemented (the reference uses NHD)")
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -201,6 +227,9 @@ class AutoKVCacheManager:
         self.layout = layout.upper()
         self.dtype_size = torch.tensor([], dtype=dtype).element_size()
         self.strict_reference_q1 = strict_reference_q1
+        if prefix_cache_rows < 0 or (prefix_cache_rows and strict_reference_q1):
+            raise ValueError("prefix_cache_rows must be >= 0, and the prefix cache needs full last pages "
+                             "(strict_reference_q1=False)")
         self.mask_penalty = torch.ones(self.seq_lens, vocab_size, dtype=dtype, device=self.device)
 
         if total_gpu_mem_bytes is None:
@@ -213,10 +242,11 @@ class AutoKVCacheManager:
                                     dtype=dtype, device=self.device)
 
         # device pool: free-page stack (bottom = page 0) and one page-list row per sequence
-        # slot, plus a last row for the CUDA-graph padding pages
+        # slot, then a row for the CUDA-graph padding pages, then the prefix cache's rows
         self._stack = torch.arange(self.max_blocks, dtype=torch.int32, device=self.device)
         self._n_free = self.max_blocks
-        self._rows = self.seq_lens + 1
+        self._pad_row = self.seq_lens
+        self._rows = self.seq_lens + 1 + prefix_cache_rows
         self._stride = max(1, min(max(self.max_blocks, 1), max_pages_per_seq))
         self._table = torch.full((self._rows, self._stride), -1, dtype=torch.int32, device=self.device)
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -238,6 +268,14 @@ class AutoKVCacheManager:
         self._n_cow = 0          # copies on write queued since the last flush
         self._cow_cap = 1024
         self._pairs = torch.zeros(2 * self._cow_cap, dtype=torch.int32, device=self.device)
+        # prefix cache (an extension): the tree on the host, each insert's pages in a cache row
+        self._cache_rows = prefix_cache_rows
+        self._root = _CacheNode(None, None, None, -1, -1)
+        self._nodes: dict = {}   # id -> node
+        self._clock = 0
+        self._next_node = 0
+        self._free_crows = list(range(prefix_cache_rows))  # handed out from the end
+        self._crow_nodes: dict = {}  # cache row -> nodes homed there
 
         # host bookkeeping: counts only
         self.free_seq_lens = list(range(self.seq_lens))
@@ -355,7 +393,7 @@ class AutoKVCacheManager:
         slot, out = self._staging.host((8 if positions else 6) * b + 1)
         desc = out[: 4 * b].reshape(b, 4)
         desc[:r, 0] = slots
-        desc[r:, 0] = self._rows - 1
+        desc[r:, 0] = self._pad_row
         desc[:r, 1] = 0
         desc[r:, 1] = np.arange(b - r, dtype=np.int32)
         desc[:r, 2] = npages
@@ -420,7 +458,7 @@ class AutoKVCacheManager:
     @property
     def padding_pages(self) -> list:
         self._flush()
-        return self._table[self._rows - 1, : self._n_padding].tolist() if self._n_padding else []
+        return self._table[self._pad_row, : self._n_padding].tolist() if self._n_padding else []
 
     # ------------------------------------------------------------------ page pool (A3-A5)
 
@@ -446,21 +484,35 @@ class AutoKVCacheManager:
         n, last = self._counts(batch_id)
         return (n - 1) * self.block_size + last if n else 0
 
-    def allocate(self, batch_id, total_tokens: int, *, prefix=None) -> _Pages:
+    def allocate(self, batch_id, total_tokens: int, *, prefix=None, tokens=None) -> _Pages:
         """manager.py:99-112: pop ceil(T / block_size) pages, take a sequence slot.  With
         ``prefix`` (an extension), the pages of that live sequence covering the first
         min(T, len(prefix)) tokens come first (a partial last page included; copied, if this
-        sequence's tokens continue into it) and only the rest are popped."""
+        sequence's tokens continue into it) and only the rest are popped.  With ``tokens``
+        (the prefix cache, an extension: the sequence's token ids), the cached pages of the
+        longest page-aligned prefix of tokens[:T] come first; ``match_prefix`` tells how many
+        tokens that is beforehand.  With the prefix cache, pages only the cache holds are
+        evicted first when the free pages are too few."""
         self._end_dev()
         bs = self.block_size
-        k, cow = 0, False
+        k, cow, path = 0, False, []
         if prefix is not None:
             if prefix not in self._npages:
                 raise ValueError(f"{prefix} not allocated")
+            if tokens is not None:
+                raise ValueError("prefix and tokens are exclusive")
             ts = min(total_tokens, self._seq_len(prefix))
             k = math.ceil(ts / bs)
             cow = total_tokens > ts and ts % bs != 0
+        elif tokens is not None:
+            if not self._cache_rows:
+                raise ValueError("allocate(tokens=) needs the prefix cache (prefix_cache_rows > 0)")
+            self._clock += 1
+            path = self._match(tokens, total_tokens)
+            k = len(path)
         num_pages = math.ceil(total_tokens / bs) - k
+        if self._n_free < num_pages + cow and self._cache_rows:
+            self.evict(num_pages + cow - self._n_free, _protect=set(path))
         if self._n_free < num_pages + cow:
             raise RuntimeError("Not enough KV cache blocks available")
         if not self.free_seq_lens:
@@ -468,7 +520,14 @@ class AutoKVCacheManager:
         slot = self.free_seq_lens.pop()
         self._ensure_stride(k + num_pages)
         handles = []
-        if k:
+        if path:
+            handles = [n.handle for n in path]
+            self._hold(handles)
+            for n in path:
+                n.last = self._clock
+            # the deepest node's cache row holds the whole path from column 0
+            self._ops.append((_COPY, slot, path[-1].row, 0, k))
+        elif k:
             handles = self._pg[prefix][:k]
             self._hold(handles)
             self._ops.append((_COPY, slot, self.batch_to_seq_len[prefix], 0, k))
@@ -490,11 +549,18 @@ class AutoKVCacheManager:
         self.mask_penalty[slot] = 1.0
         return _Pages(self, slot, k + num_pages)
 
-    def free(self, batch_id) -> None:
+    def free(self, batch_id, *, tokens=None) -> None:
         """manager.py:114-120: push the pages back in page order, release the slot.  With
         shared pages (an extension), only the pages no other list holds go back: always a tail
-        of the list, since a list holding one of this sequence's pages holds all before it."""
+        of the list, since a list holding one of this sequence's pages holds all before it.
+        With ``tokens`` (the prefix cache, an extension: the sequence's token ids), its full
+        pages are first kept in the cache (see ``_insert``)."""
         self._end_dev()
+        if tokens is not None:
+            if not self._cache_rows:
+                raise ValueError("free(tokens=) needs the prefix cache (prefix_cache_rows > 0)")
+            if batch_id in self._npages:
+                self._insert(batch_id, tokens)
         handles = self._pg.pop(batch_id, [])
         n = self._npages.pop(batch_id, 0)
         self.batch_to_page_lengths.pop(batch_id, None)
@@ -524,6 +590,8 @@ class AutoKVCacheManager:
         full_new_pages = total_tokens // self.block_size
         remaining = total_tokens % self.block_size
         cow = num_new_tokens > 0 and self._shares_last_page(batch_id)
+        if full_new_pages + cow > self._n_free and self._cache_rows:
+            self.evict(full_new_pages + cow - self._n_free)
         if full_new_pages + cow > self._n_free:
             raise RuntimeError("Not enough free blocks to append tokens")
         if cow:
@@ -536,6 +604,117 @@ class AutoKVCacheManager:
             self._npages[batch_id] = col + full_new_pages
             self._pg[batch_id] += self._new_handles(full_new_pages)
         self.batch_to_page_lengths[batch_id] = remaining
+
+    # ------------------------------------------------------------------ prefix cache (extension)
+
+    def _keys(self, tokens, limit: int) -> list:
+        bs = self.block_size
+        n = min(len(tokens), limit) // bs
+        return [tuple(int(t) for t in tokens[i * bs:(i + 1) * bs]) for i in range(n)]
+
+    def _match(self, tokens, limit: int) -> list:
+        path, node = [], self._root
+        for key in self._keys(tokens, limit):
+            node = node.children.get(key)
+            if node is None:
+                break
+            path.append(node)
+        return path
+
+    def match_prefix(self, tokens) -> int:
+        """How many leading tokens of ``tokens`` the prefix cache holds (whole pages); what
+        ``allocate(..., tokens=tokens)`` would start the sequence with.  Touches nothing."""
+        if not self._cache_rows:
+            return 0
+        return len(self._match(tokens, len(tokens))) * self.block_size
+
+    @property
+    def prefix_cache_pages(self) -> int:
+        """Pages the prefix cache holds (whether or not live sequences hold them too)."""
+        return len(self._nodes)
+
+    def _insert(self, batch_id, tokens) -> None:
+        """Keep batch_id's full pages (those whose tokens ``tokens`` gives) in the cache.
+        Walking from the root, a block cached with this sequence's own page is followed, a
+        block cached with another page ends the walk, and the blocks after the last one
+        followed become new nodes holding this sequence's pages, all homed in one cache row:
+        the sequence's row up to the last new node copied there (it holds the whole path).
+        With no cache row free, least recently used pages are evicted until one is; if none
+        is, nothing is inserted."""
+        self._clock += 1
+        handles = self._pg[batch_id]
+        node, created = self._root, []
+        for i, key in enumerate(self._keys(tokens, self._seq_len(batch_id))):
+            child = node.children.get(key) if not created else None
+            if child is not None:
+                if child.handle != handles[i]:
+                    break
+                child.last = self._clock
+                node = child
+                continue
+            new = _CacheNode(key, handles[i], node, self._next_node, i)
+            self._next_node += 1
+            created.append(new)
+            node = new
+        if not created:
+            return
+        while not self._free_crows and self._evict_one(()):
+            pass
+        if not self._free_crows:
+            return
+        r = self._free_crows.pop()
+        row = self._pad_row + 1 + r
+        self._crow_nodes[row] = len(created)
+        for n in created:
+            n.parent.children[n.key] = n
+            n.row, n.last = row, self._clock
+            self._nodes[n.id] = n
+        self._hold([n.handle for n in created])
+        self._ops.append((_COPY, row, self.batch_to_seq_len[batch_id], 0, created[-1].col + 1))
+
+    def _evict_one(self, protect) -> bool:
+        best = None
+        for n in self._nodes.values():
+            if n.children or self._rc[n.handle] != 1 or n in protect:
+                continue
+            if best is None or (n.last, n.id) < (best.last, best.id):
+                best = n
+        if best is None:
+            return False
+        del best.parent.children[best.key]
+        del self._nodes[best.id]
+        self._drop(best.handle)
+        self._ops.append((_PUSH, best.row, self._n_free, best.col, 1))
+        self._n_free += 1
+        self._crow_nodes[best.row] -= 1
+        if self._crow_nodes[best.row] == 0:
+            del self._crow_nodes[best.row]
+            self._free_crows.append(best.row - self._pad_row - 1)
+        return True
+
+    def evict(self, n: int, *, _protect=()) -> int:
+        """Return up to ``n`` pages that only the prefix cache holds to the free stack, least
+        recently used first (a page is evictable once no sequence and no longer cached prefix
+        holds it); returns how many."""
+        self._end_dev()
+        k = 0
+        while k < n and self._evict_one(_protect):
+            k += 1
+        return k
+
+    def cached_prefixes(self) -> dict:
+        """page id -> the token ids of the cached prefix ending with that page (reads the
+        device; for checks)."""
+        self._flush()
+        out = {}
+        for nd in self._nodes.values():
+            keys, m = [], nd
+            while m is not self._root:
+                keys.append(m.key)
+                m = m.parent
+            page = int(self._table[nd.row, nd.col].item())
+            out[page] = [t for k in reversed(keys) for t in k]
+        return out
 
     # ------------------------------------------------------------------ page tables (A6-A9)
 
@@ -594,7 +773,7 @@ class AutoKVCacheManager:
         if self._n_free < max_bucket:
             raise RuntimeError(f"Not enough free blocks for {max_bucket} padding pages")
         self._ensure_stride(max_bucket)
-        self._ops.append((_POP, self._rows - 1, self._n_free, 0, max_bucket))
+        self._ops.append((_POP, self._pad_row, self._n_free, 0, max_bucket))
         self._n_free -= max_bucket
         self._n_padding = max_bucket
         dev = self.device
@@ -722,7 +901,7 @@ class AutoKVCacheManager:
         check(lib().pkv_pool_step(self._stack.data_ptr(), self._dev_nfree.data_ptr(), self._table.data_ptr(),
                                   self._stride, self._rows, self._cg_rows[bucket_size].data_ptr(), bucket_size,
                                   d["n"], self.block_size, self._dev_npages.data_ptr(), self._dev_plen.data_ptr(),
-                                  self._rows - 1, self._cg_desc[bucket_size].data_ptr(),
+                                  self._pad_row, self._cg_desc[bucket_size].data_ptr(),
                                   self._cg_kv_indptr[bucket_size].data_ptr(),
                                   self._cg_kv_last_page_len[bucket_size].data_ptr(),
                                   self._cg_positions[bucket_size].data_ptr(), idx.data_ptr(), idx.numel(),

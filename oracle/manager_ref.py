@@ -193,3 +193,186 @@ class RefKVCacheManager:
         if not pages:
             return 0
         return (len(pages) - 1) * self.block_size + self.batch_to_page_lengths[batch_id]
+
+
+class _Node:
+    """One cached page of a prefix tree: the page's block_size token ids (its key under its
+    parent), the page, and its last use."""
+    __slots__ = ("key", "page", "parent", "children", "last", "id", "row")
+
+    def __init__(self, key, page, parent, nid, row=None):
+        self.key, self.page, self.parent, self.id, self.row = key, page, parent, nid, row
+        self.children: dict = {}
+        self.last = 0
+
+
+class RefRadixKVCacheManager(RefKVCacheManager):
+    """The page pool with a token-keyed prefix cache (an extension: the reference frees every
+    page of a finished sequence at once, manager.py:114-120, and keeps no index of what the
+    pages hold).  The rules, which the device manager (AutoKVCacheManager with
+    ``prefix_cache_rows``) follows exactly:
+
+    * The cache is a tree of full pages: a node is one page whose block_size token ids are its
+      key under its parent; a path from the root is a page-aligned token prefix.
+    * ``allocate(b, T, tokens=ids)`` starts b with the pages of the longest cached path that
+      matches ids[:T] block by block (only blocks wholly inside both), each page's count going
+      up by one, then pops ceil(T / block_size) - k pages as ``allocate`` does.
+    * ``free(b, tokens=ids)`` first inserts b's full pages whose tokens ids gives (blocks wholly
+      inside min(len(ids), seq_len(b))): walking from the root, a block already cached with
+      b's own page is followed, a block cached with another page ends the walk, and every block
+      after the last one followed becomes a new node holding b's page (the tree's hold counts
+      like a list's).  The new nodes of one insert share one of ``cache_rows`` cache slots; with
+      none free, least recently used nodes are evicted until one is, and if none is, nothing
+      is inserted.  Then b is freed as ``free`` does: the pages the tree keeps stay allocated.
+    * A clock advances at every allocate and free given tokens; the nodes an allocate matched
+      and the nodes a free walked or created take its value.
+    * Eviction: a node whose page only the tree holds and which has no children is evictable;
+      the one with the smallest (last use, creation number) goes first, its page back on the
+      free stack; its parent may become evictable.  ``allocate`` and ``append_tokens`` evict
+      while the free stack is short of the pages they need (never the nodes the allocate
+      matched), before raising the reference's exception if it still is; evictions made stay
+      made.  ``evict(n)`` evicts up to n pages.
+    """
+
+    def __init__(self, max_blocks: int, seq_lens: int = 128, block_size: int = 16, cache_rows: int | None = None):
+        super().__init__(max_blocks, seq_lens, block_size)
+        self.root = _Node(None, None, None, -1)
+        self.clock = 0
+        self.next_id = 0
+        self.cache_rows = self.seq_lens if cache_rows is None else cache_rows
+        self.free_rows = list(range(self.cache_rows))  # handed out from the end
+        self.row_nodes: dict = {}
+        self.evicted: list = []  # pages evicted, in order
+
+    # ---- tree
+    def _keys(self, tokens, limit: int) -> list:
+        bs = self.block_size
+        n = min(len(tokens), limit) // bs
+        return [tuple(tokens[i * bs:(i + 1) * bs]) for i in range(n)]
+
+    def match(self, tokens, limit: int | None = None) -> list:
+        """The nodes of the longest cached path matching tokens (blocks within limit)."""
+        path, node = [], self.root
+        for key in self._keys(tokens, len(tokens) if limit is None else limit):
+            node = node.children.get(key)
+            if node is None:
+                break
+            path.append(node)
+        return path
+
+    def nodes(self) -> list:
+        out, stack = [], list(self.root.children.values())
+        while stack:
+            n = stack.pop()
+            out.append(n)
+            stack.extend(n.children.values())
+        return out
+
+    def cached_pages(self) -> dict:
+        """page -> the token ids of the path ending at it."""
+        out = {}
+        for n in self.nodes():
+            keys, m = [], n
+            while m is not self.root:
+                keys.append(m.key)
+                m = m.parent
+            out[n.page] = [t for k in reversed(keys) for t in k]
+        return out
+
+    def _evict_one(self, protect=()) -> bool:
+        best = None
+        for n in self.nodes():
+            if n.children or self.refs[n.page] != 1 or n in protect:
+                continue
+            if best is None or (n.last, n.id) < (best.last, best.id):
+                best = n
+        if best is None:
+            return False
+        del best.parent.children[best.key]
+        del self.refs[best.page]
+        self.free_blocks.append(best.page)
+        self.evicted.append(best.page)
+        self.row_nodes[best.row] -= 1
+        if self.row_nodes[best.row] == 0:
+            del self.row_nodes[best.row]
+            self.free_rows.append(best.row)
+        return True
+
+    def evict(self, n: int, protect=()) -> int:
+        k = 0
+        while k < n and self._evict_one(protect):
+            k += 1
+        return k
+
+    # ---- the pool's calls
+    def allocate(self, batch_id, total_tokens: int, prefix=None, tokens=None) -> list:
+        bs = self.block_size
+        if prefix is not None and prefix not in self.batch_to_blocks:
+            raise ValueError(f"{prefix} not allocated")
+        if tokens is None:
+            need = math.ceil(total_tokens / bs)
+            if prefix is not None:
+                ts = min(total_tokens, self.seq_len(prefix))
+                need += -math.ceil(ts / bs) + (total_tokens > ts and ts % bs != 0)
+            if len(self.free_blocks) < need:
+                self.evict(need - len(self.free_blocks))
+            return super().allocate(batch_id, total_tokens, prefix)
+        if prefix is not None:
+            raise ValueError("prefix and tokens are exclusive")
+        self.clock += 1
+        path = self.match(tokens, total_tokens)
+        need = math.ceil(total_tokens / bs) - len(path)
+        if len(self.free_blocks) < need:
+            self.evict(need - len(self.free_blocks), protect=set(path))
+        if len(self.free_blocks) < need:
+            raise RuntimeError("Not enough KV cache blocks available")
+        blocks = [n.page for n in path]
+        for n in path:
+            self.refs[n.page] += 1
+            n.last = self.clock
+        blocks += [self._pop() for _ in range(need)]
+        self.batch_to_blocks[batch_id] = blocks
+        page_len = total_tokens % bs
+        if page_len == 0 and total_tokens > 0:
+            page_len = bs
+        self.batch_to_page_lengths[batch_id] = page_len
+        self.batch_to_total_tokens[batch_id] = total_tokens
+        self.batch_to_seq_len[batch_id] = self.free_seq_lens.pop()
+        return blocks
+
+    def free(self, batch_id, tokens=None) -> None:
+        if tokens is not None and batch_id in self.batch_to_blocks:
+            self.clock += 1
+            blocks = self.batch_to_blocks[batch_id]
+            node, created = self.root, []
+            for i, key in enumerate(self._keys(tokens, self.seq_len(batch_id))):
+                child = node.children.get(key) if not created else None
+                if child is not None:
+                    if child.page != blocks[i]:
+                        break
+                    child.last = self.clock
+                    node = child
+                    continue
+                new = _Node(key, blocks[i], node, self.next_id)
+                self.next_id += 1
+                created.append(new)
+                node = new
+            if created:
+                while not self.free_rows and self._evict_one():
+                    pass
+                if self.free_rows:
+                    row = self.free_rows.pop()
+                    self.row_nodes[row] = len(created)
+                    for n in created:
+                        n.parent.children[n.key] = n
+                        n.row, n.last = row, self.clock
+                        self.refs[n.page] += 1
+        super().free(batch_id)
+
+    def append_tokens(self, batch_id, num_new_tokens: int) -> None:
+        if batch_id in self.batch_to_blocks:
+            t = self.batch_to_page_lengths.get(batch_id, 0) + num_new_tokens
+            need = t // self.block_size + (num_new_tokens > 0 and self.shares_last_page(batch_id))
+            if need > len(self.free_blocks):
+                self.evict(need - len(self.free_blocks))
+        super().append_tokens(batch_id, num_new_tokens)

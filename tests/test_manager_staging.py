@@ -25,6 +25,7 @@ def _mirror(ref: RefKVCacheManager) -> AutoKVCacheManager:
     m._npages = {b: len(p) for b, p in ref.batch_to_blocks.items()}
     m._n_padding = len(ref.padding_pages)
     m._rows = ref.seq_lens + 1
+    m._pad_row = ref.seq_lens
     m._dev = None
     m._staging = _HostStaging()
     return m
@@ -86,7 +87,7 @@ def test_staged_tables_match_oracle(seed):
         assert out[7 * b + 1:].tolist() == [0] * bucket
         desc = out[: 4 * b].reshape(b, 4).tolist()
         real = [[ref.batch_to_seq_len[i], 0, len(ref.batch_to_blocks[i]), 0] for i in ids]
-        pad = [[m._rows - 1, i, 1, 0] for i in range(bucket - len(ids))]
+        pad = [[m._pad_row, i, 1, 0] for i in range(bucket - len(ids))]
         assert desc == real + pad
 
 

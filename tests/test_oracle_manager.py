@@ -177,3 +177,111 @@ def test_prefix_pool_invariants(seq):
             assert counts == sorted(counts, reverse=True)
             if pages:
                 assert m.seq_len(b) == (len(pages) - 1) * 16 + m.batch_to_page_lengths[b]
+
+
+def test_radix_cache_hand_trace():
+    """The prefix cache's rules on a hand-derived trace (block_size 4, eight pages, pops from
+    the end of the free list): insert on free, match on allocate, a walk that follows its own
+    cached pages, pages the tree keeps counted like a list's, eviction only of leaves no list
+    holds (least recently used first, the parent after its child), and the exception when
+    eviction cannot make room."""
+    from oracle.manager_ref import RefRadixKVCacheManager
+    m = RefRadixKVCacheManager(8, block_size=4, cache_rows=2)
+    A = list(range(1, 11))
+    assert m.allocate("a", 10, tokens=A) == [7, 6, 5]
+    m.free("a", tokens=A)  # blocks (1..4) -> page 7 and (5..8) -> page 6 cached; page 5 freed
+    assert m.free_blocks == [0, 1, 2, 3, 4, 5]
+    assert m.cached_pages() == {7: [1, 2, 3, 4], 6: [1, 2, 3, 4, 5, 6, 7, 8]}
+    assert m.refs == {7: 1, 6: 1}
+    B = [1, 2, 3, 4, 5, 6, 7, 8, 9, 9, 9]
+    assert m.allocate("b", 11, tokens=B) == [7, 6, 5]  # two pages matched, one popped
+    assert m.refs == {7: 2, 6: 2, 5: 1}
+    assert m.allocate("c", 6, tokens=[1, 2, 3, 4, 0, 0]) == [7, 4]
+    m.free("c", tokens=[1, 2, 3, 4, 0, 0])  # follows the cached page 7; page 4 freed
+    assert m.free_blocks == [0, 1, 2, 3, 4] and m.refs == {7: 2, 6: 2, 5: 1}
+    assert m.allocate("d", 20) == [4, 3, 2, 1, 0]
+    with pytest.raises(RuntimeError, match="Not enough free blocks to append tokens"):
+        m.append_tokens("b", 2)  # nothing evictable: b holds both cached pages
+    assert m.free_blocks == [] and m.evicted == []
+    m.free("b", tokens=B)
+    assert m.free_blocks == [5] and m.refs == {7: 1, 6: 1, 4: 1, 3: 1, 2: 1, 1: 1, 0: 1}
+    assert m.allocate("e", 12) == [7, 6, 5]  # evicts page 6 (the leaf), then 7 (now a leaf)
+    assert m.evicted == [6, 7] and m.cached_pages() == {} and m.free_rows == [0, 1]
+    # the same tokens cached with another sequence's pages end the walk: nothing of g is kept
+    m.free("e")
+    m.free("d")
+    X = [9, 9, 9, 9, 8, 8, 8, 8]
+    f = m.allocate("f", 8, tokens=X)
+    g = m.allocate("g", 8, tokens=X)
+    assert f == [0, 1] and g == [2, 3]
+    m.free("f", tokens=X)
+    m.free("g", tokens=X)
+    assert m.cached_pages() == {0: [9, 9, 9, 9], 1: X}
+    assert m.free_blocks[-2:] == [2, 3]
+    # least recently used first: touch f's path, then cache another path and evict one page
+    h = m.allocate("h", 4, tokens=[5, 5, 5, 5])
+    m.free("h", tokens=[5, 5, 5, 5])
+    assert m.allocate("x", 4, tokens=X) == [0]  # touches page 0 only (one block asked for)
+    m.free("x")
+    assert m.evict(1) == 1 and m.evicted[-1] == 1  # page 1: untouched since f's free
+    assert m.evict(1) == 1 and m.evicted[-1] == h[0]  # then h's page (older than page 0's touch)
+    assert m.cached_pages() == {0: [9, 9, 9, 9]}
+
+
+radix_ops = st.lists(st.tuples(st.sampled_from(["alloc", "alloc", "append", "free", "free_plain", "evict"]),
+                               st.integers(0, 6), st.integers(0, 3), st.integers(0, 90)), max_size=60)
+
+
+@settings(max_examples=200, deadline=None)
+@given(radix_ops)
+def test_radix_cache_invariants(seq):
+    """Random allocates over a few shared token streams, appends, frees with and without
+    tokens, evictions, under pool pressure (48 pages, 3 cache rows): every page is free, held by
+    lists or kept by the tree, each count equals its lists plus the tree's hold, a matched page
+    holds exactly the tokens it was matched on, and the tree's pages hold their paths."""
+    from oracle.manager_ref import RefRadixKVCacheManager
+    P, bs = 48, 16
+    m = RefRadixKVCacheManager(P, cache_rows=3)
+    streams = [[(s * 7 + i // 40) % 5 for i in range(400)] for s in range(4)]
+    content = {}  # page -> token ids written into it
+    toks = {}
+    for kind, sid, stream, n in seq:
+        try:
+            if kind == "alloc" and sid not in m.batch_to_blocks:
+                ids = streams[stream][: 5 + n * 3]
+                T = len(ids)
+                k = len(m.match(ids, T))
+                pages = m.allocate(sid, T, tokens=ids)
+                for i, pg in enumerate(pages):
+                    block = tuple(ids[i * bs:(i + 1) * bs])
+                    if i < k:
+                        assert content[pg] == block, "a matched page holds other tokens"
+                    else:
+                        content[pg] = block
+                toks[sid] = ids
+            elif kind == "append" and sid in m.batch_to_blocks:
+                m.append_tokens(sid, n % 20)
+                toks[sid] = toks[sid] + [99] * (n % 20)
+                L = m.seq_len(sid)
+                for i, pg in enumerate(m.batch_to_blocks[sid]):
+                    content[pg] = tuple(toks[sid][i * bs:min((i + 1) * bs, L)])
+            elif kind in ("free", "free_plain") and sid in m.batch_to_blocks:
+                m.free(sid, tokens=toks[sid] if kind == "free" else None)
+                del toks[sid]
+            elif kind == "evict":
+                m.evict(n % 4)
+        except RuntimeError:
+            pass
+        tree = m.cached_pages()
+        held = {}
+        for pages in m.batch_to_blocks.values():
+            for pg in pages:
+                held[pg] = held.get(pg, 0) + 1
+        for pg in tree:
+            held[pg] = held.get(pg, 0) + 1
+        assert held == m.refs
+        assert not set(held) & set(m.free_blocks)
+        assert sorted(list(held) + m.free_blocks) == list(range(P))
+        for pg, path in tree.items():
+            assert content[pg] == tuple(path[-bs:]), "a cached page holds other tokens"
+        assert len(m.free_rows) + len(m.row_nodes) == 3
