@@ -25,9 +25,11 @@ def test_a_dropped_page_is_detected():
     exp = expected_rows(wb, True)
     ip = wb.indptr.clone()
     idx = wb.indices.clone()
-    # request 3's 10th page replaced by a page no request owns (its rows select other classes)
-    unused = sorted(set(range(wb.cache.shape[0])) - set(idx.tolist()))[0]
-    idx[int(ip[3]) + 9] = unused
+    # request 3's 10th page replaced by a page no request owns (its rows select other classes:
+    # page ids that agree mod D - 1 select the same ones, so one that does not is taken)
+    was = int(idx[int(ip[3]) + 9])
+    unused = [p for p in sorted(set(range(wb.cache.shape[0])) - set(idx.tolist())) if (p - was) % (wb.d - 1)]
+    idx[int(ip[3]) + 9] = unused[0]
     bad = workloads.PagedBatch(**{**wb.__dict__, "indices": idx})
     moved = _beyond(exp, expected_rows(bad, True), torch.bfloat16)
     assert moved > 0
