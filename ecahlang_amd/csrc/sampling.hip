@@ -605,6 +605,7 @@ __device__ __forceinline__ float key_float(uint32_t k) {
 // (a slice's ties beyond kCandCap, more candidates than the wave holds, fewer than k finite
 // logits, a kept set beyond kKeptCap) are handed back to sample_kernel through `fallback`.
 constexpr int kKeptCap = 1024;
+constexpr int kRadixBins = 2048;  // the largest digit (11 bits) of the merge's radix selection
 
 template <typename T>
 __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logits, int64_t row_stride, int vocab,
@@ -614,10 +615,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logi
   __shared__ int redi[4];
   __shared__ uint32_t redk[4];
   __shared__ uint64_t redu[4];
-  __shared__ int s_n, s_last, s_bad;
-  __shared__ int s_off[kMaxSplitTiles / kSliceTiles + 1];
-  __shared__ int s_sidx[kKeptCap];
-  __shared__ uint64_t s_smass[kKeptCap];
+  __shared__ int s_n;
   const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
   if (row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kTopKRow) return;
   const int k = top_k ? top_k[b] : top_k_all;
@@ -702,133 +700,258 @@ __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logi
       if (key[i] >= ts) {
         const int pos = atomicAdd(&s_n, 1);
         const int idx = (j0 + i / 8) * kSplitTile + 8 * (int)threadIdx.x + (i % 8);
-        __hip_atomic_store(cand + pos, ((uint64_t)(uint32_t)idx << 32) | key[i], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        cand[pos] = ((uint64_t)(uint32_t)idx << 32) | key[i];
       }
     }
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // this thread's candidate stores are complete (device-visible)
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(ws.ncand + (int64_t)b * S + s, bad ? -1 : s_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    const int old = atomicAdd(&ws.counter[b], 1);
-    s_last = old == S - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
+  if (threadIdx.x == 0) ws.ncand[(int64_t)b * S + s] = bad ? -1 : s_n;
+}
 
-  // ---- the row's last slice: the candidates of every slice
-  if (threadIdx.x == 0) {
-    int off = 0, anybad = 0;
-    for (int i = 0; i < S; ++i) {
-      const int c = __hip_atomic_load(ws.ncand + (int64_t)b * S + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_off[i] = off;
-      if (c < 0) anybad = 1;
-      off += c < 0 ? 0 : c;
+// The merge of a top-k row's candidates (the launch after split_topk_kernel), one wave per row:
+// the row's k-th largest key T* over its slices' candidates, the top-p threshold over the top-k
+// set, and the inverse CDF in vocabulary order, with sample_row's integer masses, so the token is
+// the same.  A launch of its own rather than the last slice to finish: the slice kernel then
+// holds only its slice's keys and a chip's worth of its workgroups are resident at once.
+__global__ __launch_bounds__(kWave) void split_topk_merge_kernel(int vocab, const int32_t* top_k, int32_t top_k_all,
+                                                                 const float* top_p, float top_p_all,
+                                                                 const float* uniform, int32_t* out, SplitWs ws) {
+  __shared__ int s_off[kMaxSplitTiles / kSliceTiles + 1];
+  __shared__ int s_sidx[kKeptCap];
+  __shared__ uint64_t s_smass[kKeptCap];
+  __shared__ uint32_t s_skey[kKeptCap];
+  __shared__ __align__(16) int s_hist[kRadixBins];  // (16-byte vector accesses)
+  const int b = blockIdx.x, S = split_slices(vocab);
+  if (row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kTopKRow) return;
+  const int k = top_k ? top_k[b] : top_k_all;
+  const int lane = threadIdx.x;
+  if (lane == 0) ws.fallback[b] = 0;
+  // the slices' candidate counts, 64 at a time, and their running offsets
+  int off = 0, anybad = 0;
+  for (int i0 = 0; i0 < S; i0 += kWave) {
+    const int i = i0 + lane;
+    const int c = i < S ? ws.ncand[(int64_t)b * S + i] : 0;
+    anybad |= c < 0 ? 1 : 0;
+    const int cc = c < 0 ? 0 : c;
+    int incl = cc;  // inclusive prefix over the lanes below
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      incl += lane >= o ? v : 0;
     }
-    s_off[S] = off;
-    s_bad = anybad || off == 0 || off > kWave * kMergeRegs;
+    if (i < S) s_off[i] = off + incl - cc;
+    off += __shfl(incl, kWave - 1, kWave);
   }
-  __syncthreads();
-  const int n = s_off[S];
-  if (s_bad || n > kWave * kMergeRegs) {
-    if (threadIdx.x == 0) ws.fallback[b] = 1;
+  if (lane == 0) s_off[S] = off;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the offsets are in LDS for every lane
+  __builtin_amdgcn_wave_barrier();
+  const int n = off;
+  if (wave_max_u32((uint32_t)anybad) || n == 0 || n > kWave * kMergeRegs) {
+    if (lane == 0) ws.fallback[b] = 1;
     return;
   }
-  // one wave merges (shuffle reductions, no workgroup barriers)
-  if (threadIdx.x >= kWave) return;
-  const int lane = threadIdx.x;
   auto wsum_i = [](int v) __attribute__((always_inline)) { return wave_sum_i32(v); };
   auto wmax_u = [](uint32_t v) __attribute__((always_inline)) { return wave_max_u32(v); };
   uint32_t ck[kMergeRegs];
   int cidx[kMergeRegs];
+  // the slice holding candidate lane + 64 r and its first candidate's offset: the slices' offsets
+  // come to every lane through scalar registers (one readlane each), in slice order
+  int csl[kMergeRegs], cso[kMergeRegs];
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) csl[r] = cso[r] = 0;
+  for (int i0 = 0; i0 < S; i0 += kWave) {
+    const int offv = i0 + lane < S ? s_off[i0 + lane] : 0;
+    const int nin = min(kWave, S - i0);
+    for (int ii = 0; ii < nin; ++ii) {
+      const int oi = __builtin_amdgcn_readlane(offv, ii);
+#pragma unroll
+      for (int r = 0; r < kMergeRegs; ++r) {
+        if (oi <= min(lane + kWave * r, n - 1)) {
+          csl[r] = i0 + ii;
+          cso[r] = oi;
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int r = 0; r < kMergeRegs; ++r) {  // unconditional loads of clamped candidates
     const int ci = min(lane + kWave * r, n - 1);
-    int lo = 0, hi = S;  // the slice holding candidate ci: s_off[lo] <= ci < s_off[lo + 1]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_off[mid] <= ci) lo = mid; else hi = mid;
-    }
-    const uint64_t v = __hip_atomic_load(ws.cand + ((int64_t)b * S + lo) * kCandCap + (ci - s_off[lo]),
-                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t v = ws.cand[((int64_t)b * S + csl[r]) * kCandCap + (ci - cso[r])];
     const bool real = lane + kWave * r < n;
     ck[r] = real ? (uint32_t)v : 0u;
     cidx[r] = (int)(v >> 32);
   }
-  auto ccount = [&](uint32_t t) __attribute__((always_inline)) -> int {
-    int c = 0;
-#pragma unroll
-    for (int r = 0; r < kMergeRegs; ++r) c += ck[r] >= t ? 1 : 0;
-    return wsum_i(c);
-  };
   uint32_t mxk = 0;
+  int nfin = 0;
 #pragma unroll
-  for (int r = 0; r < kMergeRegs; ++r) mxk = max(mxk, ck[r]);
+  for (int r = 0; r < kMergeRegs; ++r) {
+    mxk = max(mxk, ck[r]);
+    nfin += ck[r] != 0u ? 1 : 0;
+  }
   mxk = wmax_u(mxk);
-  if (ccount(1) < k) {  // K would take NaN logits: not a candidate case
+  if (wsum_i(nfin) < k) {  // K would take NaN logits: not a candidate case
     if (lane == 0) ws.fallback[b] = 1;
     return;
   }
-  // the k-th largest key T* (ties kept)
-  uint32_t thr;
-  {
-    uint32_t lo = 1, hi = mxk + 1u;
-    while (hi - lo > 1u) {
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      if (ccount(mid) >= k) lo = mid; else hi = mid;
+  // The k-th largest key T* (ties kept): the largest T with #{key >= T} >= k, by radix
+  // selection over the bits in which the candidates' keys differ (the others are those of the
+  // largest key, and so of T*), in digits of up to 11 bits from the most significant: a
+  // histogram of the candidates that agree with the digits chosen so far, then the digit at
+  // which the count from the top reaches k.  One to three histograms replace the up to 32
+  // halvings of a bisection, each of which was a wave-wide reduction in turn.
+  uint32_t diff = 0;  // the bits in which some finite candidate differs from the largest
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) diff |= ck[r] != 0u ? ck[r] ^ mxk : 0u;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) diff |= (uint32_t)__shfl_xor((int)diff, o, kWave);
+  diff = (uint32_t)__builtin_amdgcn_readfirstlane((int)diff);
+  uint32_t thr = mxk;
+  if (diff != 0u) {
+    const int top = 32 - __builtin_clz(diff), bot = __builtin_ctz(diff);  // bits [bot, top) vary
+    thr = mxk & ~((top == 32 ? ~0u : ((1u << top) - 1u)) & ~((1u << bot) - 1u));
+    int above = 0;  // candidates above the digits chosen so far
+    for (int hi = top; hi > bot;) {
+      const int width = min(hi - bot, 11), shift = hi - width;
+      const uint32_t nb = 1u << width;
+      const uint32_t himask = hi == 32 ? 0u : ~0u << hi;  // the bits above this digit
+      hi = shift;
+      int4* hv = reinterpret_cast<int4*>(s_hist + lane * 32);  // this lane's 32 bins, 4 a vector
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hv[i] = make_int4(0, 0, 0, 0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = 0; r < kMergeRegs; ++r)
+        if (ck[r] != 0u && (ck[r] & himask) == (thr & himask))
+          atomicAdd(&s_hist[(ck[r] >> shift) & (nb - 1u)], 1);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      // this lane's bins [32 lane, 32 lane + 32), in registers; the count in the bins of the
+      // lanes above
+      int bins[32];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int4 v = hv[i];
+        bins[4 * i] = v.x;
+        bins[4 * i + 1] = v.y;
+        bins[4 * i + 2] = v.z;
+        bins[4 * i + 3] = v.w;
+      }
+      int own = 0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) own += bins[i];
+      int incl = own;  // bins of this lane and every lane above it
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_down(incl, o, kWave);
+        incl += lane + o < kWave ? v : 0;
+      }
+      const bool mine = above + incl >= k && above + incl - own < k;
+      int dig = 0, abv = 0;
+      {
+        int acc = above + incl - own;
+        bool found = false;
+#pragma unroll
+        for (int i = 31; i >= 0; --i) {
+          const bool hit = !found && acc + bins[i] >= k;
+          dig = hit ? lane * 32 + i : dig;
+          abv = hit ? acc : abv;
+          found = found || hit;
+          acc += bins[i];
+        }
+      }
+      const uint64_t who = __ballot(mine);
+      const int src = (int)__builtin_ctzll(who);
+      dig = __shfl(dig, src, kWave);
+      above = __shfl(abv, src, kWave);
+      thr |= (uint32_t)dig << shift;
     }
-    thr = lo;
   }
   const float mx = key_float(mxk);
-  uint64_t cm[kMergeRegs];  // candidate masses (0 below T*)
-#pragma unroll
-  for (int r = 0; r < kMergeRegs; ++r) cm[r] = ck[r] >= thr ? fmass(key_float(ck[r]), mx) : 0;
-  auto cmass = [&](uint32_t t) __attribute__((always_inline)) -> uint64_t {  // mass{key >= t}, t >= T*
-    uint64_t m = 0;
-#pragma unroll
-    for (int r = 0; r < kMergeRegs; ++r) m += ck[r] >= t ? cm[r] : 0;
-    return wave_sum_u64(m);
-  };
-  const float pp = top_p ? top_p[b] : top_p_all;
-  if (pp < 1.f) {
-    const uint64_t mkk = cmass(thr);
-    const double needd = ceil((double)fmaxf(pp, 0.f) * (double)mkk);
-    uint64_t need = needd < 1.0 ? 1 : (uint64_t)needd;
-    if (need > mkk) need = mkk;
-    if (mkk > 0) {  // the largest T with mass{key >= T} >= need
-      uint32_t lo = thr, hi = mxk + 1u;
-      while (hi - lo > 1u) {
-        const uint32_t mid = lo + ((hi - lo) >> 1);
-        if (cmass(mid) >= need) lo = mid; else hi = mid;
-      }
-      thr = lo;
-    }
-  }
-  // the kept set, compacted into LDS in a fixed order (ballots), then the inverse CDF in
-  // vocabulary order
-  uint64_t ms = 0;
+  // the top-k set K, compacted into LDS in a fixed order (ballots): index, key, mass
+  uint64_t kmass = 0;
   int m = 0;
 #pragma unroll
   for (int r = 0; r < kMergeRegs; ++r) {
     const bool keep = ck[r] >= thr;
     const uint64_t bal = __ballot(keep);
+    const uint64_t cm = keep ? fmass(key_float(ck[r]), mx) : 0;
     if (keep) {
       const int pos = m + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
       if (pos < kKeptCap) {
         s_sidx[pos] = cidx[r];
-        s_smass[pos] = cm[r];
+        s_skey[pos] = ck[r];
+        s_smass[pos] = cm;
       }
-      ms += cm[r];
     }
+    kmass += cm;
     m += __popcll(bal);
   }
-  ms = wave_sum_u64(ms);
+  kmass = wave_sum_u64(kmass);
   if (m > kKeptCap) {
     if (lane == 0) ws.fallback[b] = 1;
     return;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // K is in LDS for every lane
+  __builtin_amdgcn_wave_barrier();
+  // The top-p threshold over K: the largest T with mass{key >= T} >= need, which is the key of
+  // one of K's members; each lane weighs its members' keys over all of K.
+  uint64_t ms = kmass;
+  const float pp = top_p ? top_p[b] : top_p_all;
+  if (pp < 1.f && kmass > 0) {
+    const double needd = ceil((double)fmaxf(pp, 0.f) * (double)kmass);
+    uint64_t need = needd < 1.0 ? 1 : (uint64_t)needd;
+    if (need > kmass) need = kmass;
+    uint32_t tp = 0;
+    for (int e0 = 0; e0 < m; e0 += kWave) {
+      const int e = e0 + lane;
+      const uint32_t ke = e < m ? s_skey[e] : ~0u;
+      uint64_t f = 0;  // mass{key >= ke} over K, its members taken 64 at a time through readlane
+      for (int x0 = 0; x0 < m; x0 += kWave) {
+        const uint32_t kx = x0 + lane < m ? s_skey[x0 + lane] : 0u;
+        const uint64_t mx2 = x0 + lane < m ? s_smass[x0 + lane] : 0;
+        const uint32_t mlo = (uint32_t)mx2, mhi = (uint32_t)(mx2 >> 32);
+        const int nx = min(kWave, m - x0);
+#pragma unroll 8
+        for (int xx = 0; xx < nx; ++xx) {
+          const uint32_t kk = (uint32_t)__builtin_amdgcn_readlane(kx, xx);
+          const uint64_t mm = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(mhi, xx) << 32) |
+                              (uint64_t)(uint32_t)__builtin_amdgcn_readlane(mlo, xx);  // (readlane is signed)
+          f += kk >= ke ? mm : 0;
+        }
+      }
+      if (e < m && f >= need) tp = max(tp, ke);
+    }
+    tp = wmax_u(tp);
+    if (tp > thr) {  // the kept set shrinks to S = {key >= tp}: recompact it in place, in order
+      thr = tp;
+      int n2 = 0;
+      uint64_t m2 = 0;
+      for (int e0 = 0; e0 < m; e0 += kWave) {
+        const int e = e0 + lane;
+        const bool keep = e < m && s_skey[e] >= thr;
+        const int ie = keep ? s_sidx[e] : 0;
+        const uint32_t kk = keep ? s_skey[e] : 0u;
+        const uint64_t mm = keep ? s_smass[e] : 0;
+        const uint64_t bal = __ballot(keep);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();  // (every lane has read its entry before any is moved)
+        if (keep) {
+          const int pos = n2 + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+          s_sidx[pos] = ie;
+          s_skey[pos] = kk;
+          s_smass[pos] = mm;
+        }
+        m2 += mm;
+        n2 += __popcll(bal);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+      }
+      m = n2;
+      ms = wave_sum_u64(m2);
+    }
   }
   if (ms == 0) {
     if (lane == 0) out[b] = -1;
@@ -839,11 +962,26 @@ __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logi
   const double uu = fminf(fmaxf(uniform[b], 0.f), 1.f);
   uint64_t target = (uint64_t)(uu * (double)ms);
   if (target >= ms) target = ms - 1;
-  for (int e = lane; e < m; e += kWave) {
-    const int ie = s_sidx[e];
-    uint64_t pre = 0;  // mass of the kept logits before this one in vocabulary order
-    for (int f = 0; f < m; ++f) pre += s_sidx[f] < ie ? s_smass[f] : 0;
-    if (s_smass[e] > 0 && pre <= target && target < pre + s_smass[e]) out[b] = ie;
+  for (int e0 = 0; e0 < m; e0 += kWave) {
+    const int e = e0 + lane;
+    const int ie = e < m ? s_sidx[e] : 0x7fffffff;
+    const uint64_t me = e < m ? s_smass[e] : 0;
+    uint64_t pre = 0;  // mass of the kept logits before this one in vocabulary order, their members
+                       // taken 64 at a time through readlane
+    for (int f0 = 0; f0 < m; f0 += kWave) {
+      const int fi = f0 + lane < m ? s_sidx[f0 + lane] : 0x7fffffff;
+      const uint64_t fm = f0 + lane < m ? s_smass[f0 + lane] : 0;
+      const uint32_t flo = (uint32_t)fm, fhi = (uint32_t)(fm >> 32);
+      const int nf = min(kWave, m - f0);
+#pragma unroll 8
+      for (int ff = 0; ff < nf; ++ff) {
+        const int ii = __builtin_amdgcn_readlane(fi, ff);
+        const uint64_t mm = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(fhi, ff) << 32) |
+                            (uint64_t)(uint32_t)__builtin_amdgcn_readlane(flo, ff);  // (readlane is signed)
+        pre += ii < ie ? mm : 0;
+      }
+    }
+    if (e < m && me > 0 && pre <= target && target < pre + me) out[b] = ie;
   }
 }
 
@@ -865,15 +1003,20 @@ int launch_sample(const T* logits, int64_t row_stride, int rows, int vocab, cons
   if (split) {
     w = split_ws(ws, rows, vocab);
     const dim3 grid((unsigned)split_slices(vocab), (unsigned)rows);
-    // (split_max_kernel also resets every row's counter and fallback flag for the kernels below)
-    hipLaunchKernelGGL(split_max_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
-                       top_k_all, top_p, top_p_all, w);
-    if (any_whole)
+    // (split_max_kernel also resets every row's counter and fallback flag for the kernels below;
+    // the top-k merge sets its rows' flags itself, so a batch of top-k rows alone skips it)
+    if (any_whole) {
+      hipLaunchKernelGGL(split_max_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
+                         top_k_all, top_p, top_p_all, w);
       hipLaunchKernelGGL(split_sample_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
                          top_k_all, top_p, top_p_all, uniform, out, w);
-    if (any_topk)
+    }
+    if (any_topk) {
       hipLaunchKernelGGL(split_topk_kernel<T>, grid, dim3(kSplitThreads), 0, s, logits, row_stride, vocab, top_k,
                          top_k_all, top_p, top_p_all, uniform, out, w);
+      hipLaunchKernelGGL(split_topk_merge_kernel, dim3((unsigned)rows), dim3(kWave), 0, s, vocab, top_k, top_k_all,
+                         top_p, top_p_all, uniform, out, w);
+    }
   }
   if (!split || any_other || any_topk)  // (top-k rows may be handed back)
     hipLaunchKernelGGL(sample_kernel<T>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab, top_k,
