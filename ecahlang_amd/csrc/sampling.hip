@@ -608,25 +608,29 @@ constexpr int kKeptCap = 1024;
 constexpr int kRadixBins = 2048;  // the largest digit (11 bits) of the merge's radix selection
 
 template <typename T>
-__global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logits, int64_t row_stride, int vocab,
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(5))) void split_topk_kernel(
+    const T* logits, int64_t row_stride, int vocab,
                                                                    const int32_t* top_k, int32_t top_k_all,
                                                                    const float* top_p, float top_p_all,
                                                                    const float* uniform, int32_t* out, SplitWs ws) {
-  __shared__ int redi[4];
-  __shared__ uint32_t redk[4];
-  __shared__ uint64_t redu[4];
-  __shared__ int s_n;
+  __shared__ __align__(16) int s_h[kRadixBins];
+  __shared__ int s_wsum[kSplitThreads / kWave];
+  __shared__ int s_n, s_dig, s_above, s_cnt, s_total;
   const int s = blockIdx.x, b = blockIdx.y, S = gridDim.x, ntiles = split_tiles(vocab);
   if (row_kind(b, vocab, top_k, top_k_all, top_p, top_p_all) != kTopKRow) return;
   const int k = top_k ? top_k[b] : top_k_all;
   const T* p = logits + (int64_t)b * row_stride;
   const bool vec = ((uintptr_t)p % 16) == 0;
-  if (threadIdx.x == 0) s_n = 0;
+  const int t = threadIdx.x, lane = t & (kWave - 1), wv = t / kWave;
   // the slice's keys (0: past the row's end, or NaN)
   const int j0 = s * kSliceTiles, j1 = min(j0 + kSliceTiles, ntiles);
   SliceLoad<T> sl;
   sl.issue(p, vocab, vec, j0, j1);
-  uint32_t key[kSliceTiles * 8];
+  // The slice's keys, cut to their 16 most significant bits (still in the logits' order, ties
+  // merged) and packed two to a register: key i in the half i & 1 of kp[i / 2] (0: past the
+  // row's end, or NaN).  Held as 16 bits, every slice's workgroup of the batch is resident at
+  // once; a candidate's full key is recomputed from its logit when it is handed over.
+  uint32_t kp[kSliceTiles * 4];
 #pragma unroll
   for (int jj = 0; jj < kSliceTiles; ++jj) {
     float x[8];
@@ -638,74 +642,97 @@ __global__ __launch_bounds__(kSplitThreads) void split_topk_kernel(const T* logi
       for (int e = 0; e < 8; ++e) ok[e] = false;
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) key[jj * 8 + e] = ok[e] ? fkey(x[e]) : 0u;
+    for (int e = 0; e < 8; e += 2)
+      kp[jj * 4 + e / 2] = (ok[e] ? fkey(x[e]) >> 16 : 0u) | (ok[e + 1] ? fkey(x[e + 1]) & 0xFFFF0000u : 0u);
   }
-  auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {  // #{key >= t}, t >= 1
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < kSliceTiles * 8; ++i) c += key[i] >= t ? 1 : 0;
-    return block_sum_i256(c, redi);
+  auto key16 = [&](int i) __attribute__((always_inline)) -> uint32_t {
+    return (i & 1) ? kp[i >> 1] >> 16 : kp[i >> 1] & 0xFFFFu;
   };
-  uint32_t mk = 0;
+  // The threshold t_s: the start of the range of 16-bit keys (a digit of 11 bits, then one of 5)
+  // that holds the slice's k-th largest, refined until at most 2k keys lie at or above it: each
+  // level histograms, in LDS, the keys inside the range chosen so far, and one scan of the
+  // histogram finds the digit (where a bisection counted every key once per halving, with a
+  // workgroup reduction each time).  Keys at or above t_s include every logit at or above the
+  // slice's k-th largest, so every logit at or above the row's k-th largest is a candidate.
+  uint32_t ts = 1u, prefix = 0u, himask = 0u;
+  int above = 0, cnt = 0;
+#pragma unroll 1
+  for (int level = 0; level < 2; ++level) {
+    const int shift = level == 0 ? 5 : 0;
+    const uint32_t nb = level == 0 ? 2048u : 32u;
 #pragma unroll
-  for (int i = 0; i < kSliceTiles * 8; ++i) mk = max(mk, key[i]);
-  mk = block_max_u256(mk, redk);
-  // hand over between k and 2k logits (fewer candidates keep the row's merge in one wave)
-  uint32_t ts = 1;
-  int cts = count_ge(1);
-  if (cts > 2 * k) {  // (uniform) bisect: count(lo) >= k > count(hi)
-    // first by value, between the slice's smallest and largest logits (for a smooth spread of
-    // logits this reaches the k..2k band in fewer steps than halving the key range), then by key
-    uint32_t mn_inv = 0;
+    for (int i = 0; i < kRadixBins / kSplitThreads / 4; ++i)
+      reinterpret_cast<int4*>(s_h)[t * (kRadixBins / kSplitThreads / 4) + i] = make_int4(0, 0, 0, 0);
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kSliceTiles * 8; ++i) mn_inv = max(mn_inv, key[i] ? ~key[i] : 0u);
-    mn_inv = block_max_u256(mn_inv, redk);
-    uint32_t lo = ~mn_inv, hi = mk + 1u;  // count(lo) = cts (every non-NaN logit)
-    bool done = false;
-    for (int it = 0; it < 8 && hi - lo > 1u; ++it) {
-      const float fl = key_float(lo), fh = key_float(hi - 1u);
-      if (!(fabsf(fl) <= 3.4e38f) || !(fabsf(fh) <= 3.4e38f)) break;  // non-finite ends: by key
-      const uint32_t mid = fkey(fl + 0.5f * (fh - fl));
-      if (mid <= lo || mid >= hi) break;
-      const int c = count_ge(mid);
-      if (c >= k) {
-        lo = mid;
-        cts = c;
-        if (c <= 2 * k) {
-          done = true;
+    for (int i = 0; i < kSliceTiles * 8; ++i) {
+      const uint32_t kk = key16(i);
+      if (kk != 0u && (kk & himask) == prefix) atomicAdd(&s_h[(kk >> shift) & (nb - 1u)], 1);
+    }
+    __syncthreads();
+    // thread t owns bins [8t, 8t + 8); the count in its bins and in every bin above them
+    int bins[8];
+    {
+      const int4 a = reinterpret_cast<const int4*>(s_h)[2 * t], c = reinterpret_cast<const int4*>(s_h)[2 * t + 1];
+      bins[0] = a.x; bins[1] = a.y; bins[2] = a.z; bins[3] = a.w;
+      bins[4] = c.x; bins[5] = c.y; bins[6] = c.z; bins[7] = c.w;
+    }
+    int own = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) own += bins[e];
+    int incl = own;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_down(incl, o, kWave);
+      incl += lane + o < kWave ? v : 0;
+    }
+    if (lane == 0) s_wsum[wv] = incl;
+    __syncthreads();
+    for (int w2 = wv + 1; w2 < kSplitThreads / kWave; ++w2) incl += s_wsum[w2];
+    if (t == 0) s_total = incl;  // (thread 0's: every key in the range)
+    if (above + incl >= k && above + incl - own < k) {  // the thread whose bins hold the k-th largest
+      int acc = above + incl - own;
+#pragma unroll
+      for (int e = 7; e >= 0; --e) {
+        if (acc + bins[e] >= k) {
+          s_dig = 8 * t + e;
+          s_above = acc;
+          s_cnt = acc + bins[e];
           break;
         }
-      } else {
-        hi = mid;
+        acc += bins[e];
       }
     }
-    while (!done && hi - lo > 1u) {
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      const int c = count_ge(mid);
-      if (c >= k) {
-        lo = mid;
-        cts = c;
-        if (c <= 2 * k) break;
-      } else {
-        hi = mid;
-      }
+    __syncthreads();
+    if (level == 0 && s_total < k) {  // (uniform) fewer than k finite keys: all of them
+      ts = 1u;
+      cnt = s_total;
+      break;
     }
-    ts = lo;
+    cnt = s_cnt;
+    prefix |= (uint32_t)s_dig << shift;
+    himask |= (nb - 1u) << shift;
+    above = s_above;
+    ts = prefix;
+    if (cnt <= 2 * k) break;  // (uniform) at most 2k keys at or above ts
+    __syncthreads();  // (s_dig, s_above, s_cnt read by every thread before the next level writes them)
   }
-  const bool bad = cts > kCandCap;  // (ties at the threshold beyond the slice's capacity)
+  const bool bad = cnt > kCandCap;  // (ties at the threshold beyond the slice's capacity)
+  if (t == 0) s_n = 0;
+  __syncthreads();
   uint64_t* cand = ws.cand + ((int64_t)b * S + s) * kCandCap;
   if (!bad) {
 #pragma unroll
     for (int i = 0; i < kSliceTiles * 8; ++i) {
-      if (key[i] >= ts) {
+      if (key16(i) >= ts) {
         const int pos = atomicAdd(&s_n, 1);
-        const int idx = (j0 + i / 8) * kSplitTile + 8 * (int)threadIdx.x + (i % 8);
-        cand[pos] = ((uint64_t)(uint32_t)idx << 32) | key[i];
+        const int idx = (j0 + i / 8) * kSplitTile + 8 * t + (i % 8);
+        cand[pos] = ((uint64_t)(uint32_t)idx << 32) | fkey(to_f32(p[idx]));
       }
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) ws.ncand[(int64_t)b * S + s] = bad ? -1 : s_n;
+  if (t == 0) ws.ncand[(int64_t)b * S + s] = bad ? -1 : s_n;
 }
 
 // The merge of a top-k row's candidates (the launch after split_topk_kernel), one wave per row:
