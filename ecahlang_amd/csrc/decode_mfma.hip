@@ -123,6 +123,29 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     return pid >= 0 && (int64_t)pid < P.num_pages;
   };
 
+  // Prefix items (cascade schedules): every wave attends one KV head; a column is (sequence,
+  // query head of that head), 16 / g sequences per 16-column block, NB = 2 blocks per wave (1
+  // when that would exceed kMaxGroup), so G = W * NB * (16 / g) sequences share an item.
+  const int i_spb = 16 / g, i_sib = lr / g, i_gi = lr - i_sib * g;
+  const int i_nb = W * 2 * i_spb <= kMaxGroup ? 2 : 1;
+  struct ItemRegs {
+    int hv = 0;
+    int pid[2] = {0, 0};
+    int4 sv[2];
+  };
+  auto load_item = [&](int w) __attribute__((always_inline)) -> ItemRegs {
+    const int32_t* pr = P.sched_pref + (int64_t)w * kPrecStride;
+    ItemRegs r;
+    r.hv = pr[lane];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = (i_nb * wave + k) * i_spb + i_sib;
+      r.sv[k] = *reinterpret_cast<const int4*>(pr + kPrecSegOff + 4 * (e < kMaxGroup ? e : kMaxGroup - 1));
+      r.pid[k] = pr[kPrecPidOff + 64 * k + lane];
+    }
+    return r;
+  };
+
   const int N0 = P.num_ctas;
   // XCD-aware range order: workgroups are dealt round-robin to the 8 XCDs, so giving each XCD a
   // run of consecutive ranges keeps a split sequence's partials mostly on one L2.
@@ -132,11 +155,16 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   // hundred instructions) then runs while they are in flight.
   int hv0 = 0, pv0 = 0;
   const bool early = w0 < P.r_cap;
+  // A prefix item's record in registers (cascade schedules): its header (lane l: word l), the
+  // segments of this lane's two member columns, and its page ids (page p: lane p % 64 of
+  // word p / 64).  Every range's slot is read: a range that carries no item ignores it.
+  ItemRegs ir0;
   if (early) {
     const int32_t* head0 = P.sched_head + (int64_t)w0 * kHeadWords;
     const int32_t* rec0 = P.sched + (int64_t)w0 * kRecStride;
     hv0 = head0[lane];
     pv0 = head0[kHeadPidOff + lane];
+    if constexpr (CASC) ir0 = load_item(w0);
     if (wave == 0) dma16(rec0 + kRecSegOff + 4 * lane, reinterpret_cast<const char*>(s_seg));
     if (wave == 1 % W) dma16(rec0 + kRecPidOff + 4 * lane, reinterpret_cast<const char*>(s_pid));
   }
@@ -216,23 +244,21 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   constexpr int NSP = W * 2 * TILE / (2 * TILE1);      // ring slots (pages)
   static_assert(NSP >= 4 && NSP % W == 0 && NSP / W <= 4, "prefix ring");
   const float scale = P.scale_log2;
-  auto prefix_item = [&](int w) __attribute__((always_inline)) {
-    const int32_t* pr = P.sched_pref + (int64_t)w * kPrecStride;
-    const int hv2 = pr[lane];
+  auto prefix_item = [&](int w, bool pre) __attribute__((always_inline)) {
+    // the record: requested at the kernel's start for the first range, else now
+    const ItemRegs ir = pre ? ir0 : load_item(w);
+    if (!pre) __builtin_amdgcn_s_waitcnt(0x0F70);
+    const int hv2 = ir.hv;
     int plen = __builtin_amdgcn_readlane(hv2, kHdrLen);
-    plen = plen < 0 ? 0 : (plen > kRangePages ? kRangePages : plen);
+    plen = plen < 0 ? 0 : (plen > kItemPages ? kItemPages : plen);
     int pn = __builtin_amdgcn_readlane(hv2, kHdrNseg);
     pn = pn < 0 ? 0 : (pn > kMaxGroup ? kMaxGroup : pn);
     int hd = __builtin_amdgcn_readlane(hv2, kHdrHead);
     hd = hd < 0 ? 0 : (hd >= P.hkv ? P.hkv - 1 : hd);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
     if (nsplit + kMaxGroup > kMaxSplit) flush_splits(true);  // room for this item's arrivals
-    lds_barrier();  // the previous readers of s_pid and of the unit buffers are done
-    for (int k = wave; k < (plen + 255) / 256; k += W)
-      dma16(pr + kPrecPidOff + 256 * k + 4 * lane, reinterpret_cast<const char*>(s_pid + 256 * k));
+    lds_barrier();  // the previous readers of the unit buffers are done
     // my columns and their sequences (segment e = (NB wave + k) * spb + column / g)
-    const int spb = 16 / g, sib = lr / g, gi = lr - sib * g;
-    const int nb = W * 2 * spb <= kMaxGroup ? 2 : 1;
+    const int spb = i_spb, sib = i_sib, gi = i_gi, nb = i_nb;
     const int qhd = hd * g + gi;                        // query head of my column
     Seg sgk[2];
     bool ok[2];
@@ -241,8 +267,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     for (int k = 0; k < 2; ++k) {
       const int e = (nb * wave + k) * spb + sib;
       ok[k] = k < nb && sib < spb && e < pn;
-      const int4 v = *reinterpret_cast<const int4*>(pr + kPrecSegOff + 4 * (ok[k] ? e : 0));
-      sgk[k] = unpack_seg(v, plen, B, P.slot_cap);
+      sgk[k] = unpack_seg(ir.sv[k], plen, B, P.slot_cap);
       const T* src = qall + (int64_t)sgk[k].b * P.q_sn + (int64_t)qhd * P.q_sh + 8 * lg;
 #pragma unroll
       for (int s = 0; s < KSH; ++s)
@@ -258,14 +283,15 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       pl[k] = 0.f;
     }
     const bool any = __ballot(ok[0] || ok[1]) != 0;
-    // the page ids and the query rows have landed; a wait the compiler sees, so it inserts none
-    // of its own for the query registers inside the page loop (one would drain the page copies)
-    wait_stores();
-    lds_barrier();
-    // one head's K and V rows of page p into its ring slot
+    // page p's id (p wave-uniform, < kItemPages)
+    auto pid_at = [&](int p) __attribute__((always_inline)) -> int {
+      return __builtin_amdgcn_readlane(p < 64 ? ir.pid[0] : ir.pid[1], p & 63);
+    };
+    // one head's K and V rows of page p into its ring slot (the query rows' loads were issued
+    // first: the compiler's wait for them, at their first use, also covers these copies)
     const int64_t hoff = (int64_t)hd * D;
     auto issue_page = [&](int p) __attribute__((always_inline)) {
-      const int pid = __builtin_amdgcn_readfirstlane(s_pid[p]);
+      const int pid = pid_at(p);
       const int64_t pg = page_ok(pid) ? pid : 0;
       char* dst = smem + (p % NSP) * 2 * TILE1;
       const T* kb = kc + pg * P.page_stride + hoff;
@@ -300,8 +326,8 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       lds_barrier();
       for (int q = p0 + NSP - step; q < p0 + NSP && q < plen; ++q)
         if (wave == q % W) issue_page(q);
-      const int pid0 = __builtin_amdgcn_readfirstlane(s_pid[p0]);
-      const int pid1 = np2 == 2 ? __builtin_amdgcn_readfirstlane(s_pid[p0 + 1]) : pid0;
+      const int pid0 = pid_at(p0);
+      const int pid1 = np2 == 2 ? pid_at(p0 + 1) : pid0;
       const bool v0 = page_ok(pid0), v1 = np2 == 2 && page_ok(pid1);
       if (!any) continue;
       // Straight-line step (no branch between the LDS reads and their products, so they can
@@ -426,13 +452,15 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     nseg = nseg < 0 ? 0 : (nseg > len ? len : nseg);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // fetch 1 complete (compiler-visible vmcnt(0))
     if (w >= rmax) break;
-    // the early copies into s_seg / s_pid stand for this range's first two fetch-2 jobs, unless a
-    // prefix item carried by the range has since reused those arrays
-    bool early_jobs = first;
+    // the early copies into s_seg / s_pid stand for this range's first two fetch-2 jobs (a prefix
+    // item keeps its record in registers and leaves those arrays alone)
+    const bool early_jobs = first;
     if constexpr (CASC) {
       if (__builtin_amdgcn_readlane(hv, kHdrPrefix)) {
-        prefix_item(w);
-        early_jobs = false;
+        prefix_item(w, first);
+        // The item's arrivals now: its G sequences' other parts are mostly still running, so
+        // their merges fall to those parts' workgroups instead of piling up on this one.
+        if (nsplit > 0) flush_splits(false);
       }
     }
     if (nseg == 0) continue;

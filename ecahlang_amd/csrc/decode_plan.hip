@@ -207,17 +207,17 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams P)
         if (pp > 0 && group) {
           np = (pp + kPrefixChunkMin - 1) / kPrefixChunkMin;
           np = np > kMaxPrefixParts ? kMaxPrefixParts : np;
-          const int need = (pp + kRangePages - 1) / kRangePages;
+          const int need = (pp + kItemPages - 1) / kItemPages;
           np = np < need ? need : np;
           if (np > kMaxPrefixNp) np = 0;  // (not grouped; its pages are still marked)
           c = np ? (pp + np - 1) / np : 0;
         }
         items = np * P.hkv * ((size + G - 1) / G);
         parts = np * size;
-        // an item reads one head's rows of C pages: C / Hkv pages' worth
-        const unsigned long long x = ((unsigned long long)c * kPrefixCostNum + (unsigned long long)kPrefixCostDen * P.hkv - 1) /
-                                     ((unsigned long long)kPrefixCostDen * P.hkv);
-        xt = (unsigned long long)items * (x > 0 ? x : 1);
+        // an item's weight in suffix pages (decode_sched.h)
+        const unsigned long long x =
+            ((unsigned long long)c * kPrefixCostNum + kPrefixCostDen - 1) / kPrefixCostDen + kPrefixItemFixed;
+        xt = (unsigned long long)items * x;
       }
       P.run_p[r] = pp;
       P.run_np[r] = np;

@@ -80,12 +80,14 @@ constexpr int kPrecSegOff = 16;                        // <= kMaxGroup segments:
 constexpr int kPrecPidOff = 256;
 constexpr int kPrecStride = kPrecPidOff + kRangePages; // words, 256-byte multiple
 constexpr int kPrefixMinPages = 16;                    // shorter shared prefixes are not grouped
-constexpr int kPrefixChunkMin = 32;                    // pages per chunk, unless that makes too many
-constexpr int kMaxPrefixParts = 4;                     // chunks per prefix (more only past 4 x 512 pages)
+constexpr int kPrefixChunkMin = 8;                     // pages per chunk, unless that makes too many
+constexpr int kMaxPrefixParts = 16;                    // chunks per prefix (more only past 16 x 128 pages)
 constexpr int kMaxPrefixNp = 31;                       // chunks per prefix at most (5 bits)
-// A prefix item's weight when the plan balances the ranges, in streamed pages: the bytes it
-// reads (one head's rows of C pages) times kPrefixCostNum / kPrefixCostDen.
-constexpr int kPrefixCostNum = 1, kPrefixCostDen = 1;
+constexpr int kItemPages = 128;                        // pages per chunk at most (ids in 2 registers a lane)
+// A prefix item's weight when the plan balances the ranges, in streamed pages (a suffix page
+// weighs 1): a fixed kPrefixItemFixed for its set-up and its arrivals, plus its C pages of one
+// head's rows times kPrefixCostNum / kPrefixCostDen (the item attends G sequences to each).
+constexpr int kPrefixCostNum = 7, kPrefixCostDen = 5, kPrefixItemFixed = 19;
 
 // Head block of the matrix-core decode: the largest power of two HB with HB * g <= 16 query heads
 // (the MFMA's 16 columns), HB * head_dim <= 256 and HB | Hkv.
