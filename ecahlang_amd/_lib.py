@@ -57,6 +57,9 @@ SIGNATURES: dict[str, tuple] = {
          _f32, _i32, _vp, _i64, _i64, _i32, _vp],
     ),
     "pkv_prefill_mfma_supported": (_i32, [_i32, _i32, _i32, _i32, _i32]),
+    "pkv_prefill_work_list": (
+        _i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _i64,
+               _vp]),
     "pkv_batch_prefill_mfma": (
         _i32,
         [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,

@@ -18,6 +18,8 @@ from __future__ import annotations
 import math
 import os
 
+import numpy as np
+
 import torch
 
 from ._lib import check, dtype_code, lib, stream_ptr
@@ -226,57 +228,52 @@ class BatchDecodeWithPagedKVCacheWrapper:
     forward = run
 
 
-def prefill_work_list(qo_indptr: list, kv_indptr: list, last_page_len: list, g: int, hkv: int, page_size: int,
+def prefill_work_list(qo_indptr, kv_indptr, last_page_len, g: int, hkv: int, page_size: int,
                       causal: bool, head_dim: int, num_cus: int, ws_bytes: int, rows: int = 256,
-                      partial_bytes: int = 4) -> dict:
-    """The matrix-core prefill kernel's work list, on the host.  Items are (request, KV head,
-    rows/g query tokens, chunk of the keys those tokens see): the 12 int32 fields
+                      partial_bytes: int = 4, chunk: int | None = None) -> dict:
+    """The matrix-core prefill kernel's work list, built on the host by the library
+    (``pkv_prefill_work_list``).  Items are (request, KV head, rows/g query tokens, chunk of the
+    keys those tokens see): the 12 int32 fields
     [b, h, t0, tq, k0, k1, slot, kv_len, qo_len, qo_start, kv_indptr[b], 0].  A key range longer
     than the chunk is cut into chunks (slot >= 0) that form a split group
     [first slot, chunks, qo_start, t0, tq, h, 0, 0], whose partials a second kernel merges.
-    Chunks are whole steps of the kernel (64 keys), sized for about one item per CU: fewer,
-    longer items split fewer key ranges (less partial traffic, a shorter merge); they are
-    doubled while the partials would not fit in ``ws_bytes``.  ``partial_bytes`` is the size of
-    one element of a partial output row: 2 for fp16 caches (the kernel keeps their partials in
-    fp16), 4 otherwise.  Items are issued longest first."""
-    tq_max = rows // g
-    groups = []  # (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b)
-    for b in range(len(qo_indptr) - 1):
-        qo_len = qo_indptr[b + 1] - qo_indptr[b]
-        npg = kv_indptr[b + 1] - kv_indptr[b]
-        kv_len = (npg - 1) * page_size + last_page_len[b] if npg > 0 else 0
-        for t0 in range(0, qo_len, tq_max):
-            tq = min(tq_max, qo_len - t0)
-            kv_end = min(kv_len, max(0, t0 + tq + kv_len - qo_len)) if causal else kv_len
-            for h in range(hkv):
-                groups.append((h, t0, tq, kv_end, kv_len, qo_len, qo_indptr[b], kv_indptr[b], b))
-    total = sum(gr[3] for gr in groups)
-    chunk = max(256, min(8192, -(-total // num_cus // 64) * 64 or 256))
-    while True:
-        items, merges, nslots = [], [], 0
-        for (h, t0, tq, kv_end, kv_len, qo_len, qo_start, kp0, b) in groups:
-            nch = max(1, -(-kv_end // chunk))
-            if nch == 1:
-                items.append([b, h, t0, tq, 0, kv_end, -1, kv_len, qo_len, qo_start, kp0, 0])
-                continue
-            for c in range(nch):
-                items.append([b, h, t0, tq, c * chunk, min(kv_end, (c + 1) * chunk), nslots + c, kv_len,
-                              qo_len, qo_start, kp0, 0])
-            merges.append([nslots, nch, qo_start, t0, tq, h, 0, 0])
-            nslots += nch
-        a = lambda n: -(-n // 256) * 256
-        off_g = a(len(items) * 12 * 4)
-        off_ml = off_g + a(len(merges) * 8 * 4)
-        off_o = off_ml + a(nslots * rows * 8)
-        need = off_o + nslots * rows * head_dim * partial_bytes
-        if need <= ws_bytes or not merges or chunk >= 8192:
-            break
-        chunk = min(8192, chunk * 2)
-    if need > ws_bytes:
-        raise RuntimeError(f"prefill workspace too small: need {need} bytes")
-    items.sort(key=lambda it: it[4] - it[5])  # longest key range first
-    return {"items": items, "groups": merges, "chunk": chunk, "slots": nslots,
-            "off_groups": off_g, "off_ml": off_ml, "off_o": off_o, "bytes": need}
+    Chunks are whole steps of the kernel (64 keys); unless ``chunk`` fixes it, the chunk is the
+    one among a few around total keys / CUs whose simulated kernel time (items longest first,
+    each to the least loaded CU) is lowest, and it is doubled while the partials would not fit
+    in ``ws_bytes``.  ``partial_bytes`` is the size of one element of a partial output row: 2
+    for fp16 caches (the kernel keeps their partials in fp16), 4 otherwise.  Items are issued
+    longest first.  ``items`` / ``groups`` are lists of records; ``items_np`` / ``groups_np``
+    the same as int32 arrays."""
+    qo = np.ascontiguousarray(np.asarray(qo_indptr, dtype=np.int64), dtype=np.int32)
+    kv = np.ascontiguousarray(np.asarray(kv_indptr, dtype=np.int64), dtype=np.int32)
+    last = np.ascontiguousarray(np.asarray(last_page_len, dtype=np.int64), dtype=np.int32)
+    B = len(qo) - 1
+    if len(kv) != B + 1 or len(last) < B:
+        raise ValueError("indptr / last_page_len lengths do not match")
+    # capacity: every (request, query tile, KV head) holds at most max(1, kv_len / 256) chunks
+    tq_max = max(1, rows // max(1, g))
+    qn = np.diff(qo.astype(np.int64))
+    npg = np.diff(kv.astype(np.int64))
+    kvl = np.where(npg > 0, (npg - 1) * page_size + last[:B], 0)
+    tiles = -(-np.maximum(qn, 0) // tq_max)
+    n_groups_cap = int((tiles * hkv).sum())
+    n_items_cap = int((tiles * hkv * np.maximum(1, -(-np.maximum(kvl, 0) // 256))).sum())
+    items = np.zeros((max(1, n_items_cap), 12), dtype=np.int32)
+    groups = np.zeros((max(1, n_groups_cap), 8), dtype=np.int32)
+    info = np.zeros(8, dtype=np.int64)
+    L = lib()
+    rc = L.pkv_prefill_work_list(qo.ctypes.data, kv.ctypes.data, last.ctypes.data, B, int(g), int(hkv),
+                                 int(page_size), 1 if causal else 0, int(head_dim), int(num_cus), int(ws_bytes),
+                                 int(rows), int(partial_bytes), int(chunk or 0), items.ctypes.data,
+                                 items.shape[0], groups.ctypes.data, groups.shape[0], info.ctypes.data)
+    if rc == -6:
+        raise RuntimeError(f"prefill workspace too small: need {int(info[7])} bytes")
+    check(int(rc), "prefill plan")
+    ni, ng = int(info[0]), int(info[1])
+    items, groups = items[:ni], groups[:ng]
+    return {"items": items.tolist(), "groups": groups.tolist(), "items_np": items, "groups_np": groups,
+            "chunk": int(info[2]), "slots": int(info[3]), "off_groups": int(info[4]), "off_ml": int(info[5]),
+            "off_o": int(info[6]), "bytes": int(info[7])}
 
 
 class BatchPrefillWithPagedKVCacheWrapper:
@@ -348,13 +345,14 @@ class BatchPrefillWithPagedKVCacheWrapper:
         wl = prefill_work_list(qo, kp, last, self._hq // self._hkv, self._hkv, self._ps, self._causal, self._d,
                                _num_cus(dev), ws_bytes, self._ROWS,
                                partial_bytes=2 if self._q_dtype == torch.float16 else 4)
-        items, merges = wl["items"], wl["groups"]
+        items, merges = wl["items_np"], wl["groups_np"]
         off_g, off_ml, off_o = wl["off_groups"], wl["off_ml"], wl["off_o"]
-        flat = [x for it in items for x in it] + [0] * ((off_g - len(items) * 48) // 4) + \
-               [x for m in merges for x in m]
-        if flat:
-            host = torch.tensor(flat, dtype=torch.int32).pin_memory()
-            self._workspace.view(torch.uint8)[: 4 * len(flat)].view(torch.int32).copy_(host, non_blocking=True)
+        if len(items):
+            flat = np.zeros(off_g // 4 + merges.size, dtype=np.int32)
+            flat[: items.size] = items.reshape(-1)
+            flat[off_g // 4:] = merges.reshape(-1)
+            host = torch.from_numpy(flat).pin_memory()
+            self._workspace.view(torch.uint8)[: 4 * flat.size].view(torch.int32).copy_(host, non_blocking=True)
         base = self._workspace.data_ptr()
         self._n_items, self._n_groups = len(items), len(merges)
         self._items_ptr, self._groups_ptr = base, base + off_g

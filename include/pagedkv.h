@@ -257,6 +257,22 @@ int pkv_batch_prefill_valu(const void* q, int64_t q_stride_n, int64_t q_stride_h
  * aligned (PKV_E_ALIGN otherwise). */
 int pkv_prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t num_qo_heads,
                                int32_t num_kv_heads, int32_t page_size);
+/* The host half of BatchPrefillWithPagedKVCacheWrapper.plan (ecahlang/main.py:432-443; host
+ * memory in and out, no device call): the work list pkv_batch_prefill_mfma takes, for a batch of
+ * `batch` requests (qo_indptr, kv_indptr [batch + 1], kv_last_page_len [batch]) with GQA group
+ * `group` and `rows` query rows per item.  chunk: keys per item (a multiple of 64 in
+ * [256, 8192]), or 0 to pick the one with the lowest simulated kernel time among chunks around
+ * total keys / num_cus, doubled while the split partials (partial_bytes per element: 2 or 4)
+ * would not fit in workspace_bytes.  Writes the items (12 int32 each, longest key range first)
+ * and split groups (8 int32 each) and info[8] = {n_items, n_groups, chunk, slots, byte offset
+ * of the groups, of part_ml, of part_o, workspace bytes needed}.  Returns 0, PKV_E_WORKSPACE
+ * (info filled) or PKV_E_ARG (bad arguments, or more records than items_cap / groups_cap). */
+int pkv_prefill_work_list(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                          const int32_t* kv_last_page_len, int32_t batch, int32_t group,
+                          int32_t num_kv_heads, int32_t page_size, int32_t causal, int32_t head_dim,
+                          int32_t num_cus, int64_t workspace_bytes, int32_t rows,
+                          int32_t partial_bytes, int32_t chunk, int32_t* items, int64_t items_cap,
+                          int32_t* groups, int64_t groups_cap, int64_t* info);
 int pkv_batch_prefill_mfma(const void* q, int64_t q_stride_n, int64_t q_stride_h,
                            const void* k_cache, const void* v_cache, int64_t page_stride,
                            int64_t num_pages, const int32_t* kv_indices, int64_t num_indices,
