@@ -613,16 +613,17 @@ def step36(args, torch, workloads, dev):
     steps, warmup = max(1, min(args.steps, 40)), max(1, min(args.warmup, 4))
     print("bench: building the 36-layer shared-prefix decode loop (B=128)", file=sys.stderr, flush=True)
     device_steps = not args.host_steps
+    cascade = not args.no_cascade
     n_prof = args.profile_launches
     loop = workloads.SharedPrefixDecodeLoop(dev, max_steps=(n_prof or 2 * steps) + warmup + 2,
-                                            device_steps=device_steps)
+                                            device_steps=device_steps, cascade=cascade)
     for _ in range(warmup):
         loop.begin_step()
         loop.replay()
         loop.retire()
     torch.cuda.synchronize()
     step_key = {"layers": loop.layers, "batch": loop.batch, "prefix_tokens": loop.prefix_tokens,
-                "device_steps": device_steps}
+                "device_steps": device_steps, "cascade": cascade}
     if n_prof:  # counter runs: n steps (36 decode launches each), then copies of a layer's unique bytes
         ub, lb = [], []
         for _ in range(n_prof):
@@ -985,6 +986,9 @@ def main():
     ap.add_argument("--ctas", type=int, default=None, help="decode workgroups (default: one per CU)")
     ap.add_argument("--host-steps", action="store_true",
                     help="shared-prefix step: page-table bookkeeping on the host each step (the reference's loop)")
+    ap.add_argument("--no-cascade", action="store_true",
+                    help="shared-prefix step: plan without prefix items (every sequence reads the prefix, "
+                         "kept in L2 by the hint)")
     ap.add_argument("--dynamic", action="store_true",
                     help="waves take pages on demand (faster, not bitwise reproducible)")
     ap.add_argument("--workload", default="qwen25_3b_b64",

@@ -280,11 +280,12 @@ int batch_decode(const void* q, int64_t q_stride_n, int64_t q_stride_h, const Ap
       decode_mfma_supported(dtype, head_dim, g, num_kv_heads, batch)) {
     if (app) {
       // The append rides in the decode kernel (the wave that attends a sequence's last page
-      // writes the token there) for the fixed page order of a plain schedule and 16-byte rows;
-      // otherwise it is a launch of its own before the decode.
+      // writes the token there) for the fixed page order of the plan's ranges and 16-byte rows
+      // (the page that receives the token is never part of a shared prefix: the plan keeps it
+      // in the sequence's own pages); otherwise it is a launch of its own before the decode.
       const uintptr_t m = (uintptr_t)app->k | (uintptr_t)app->v;
       const int64_t st = (app->k_sn | app->k_sh | app->v_sn | app->v_sh) * es;
-      if (!P.dynamic && !P.cascade && m % 16 == 0 && st % 16 == 0) {
+      if (!P.dynamic && m % 16 == 0 && st % 16 == 0) {
         P.ak = (const char*)app->k;
         P.av = (const char*)app->v;
         P.ak_sn = app->k_sn * es, P.ak_sh = app->k_sh * es, P.av_sn = app->v_sn * es, P.av_sh = app->v_sh * es;

@@ -123,11 +123,10 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     return pid >= 0 && (int64_t)pid < P.num_pages;
   };
 
-  // Prefix items (cascade schedules): every wave attends one KV head; a column is (sequence,
-  // query head of that head), 16 / g sequences per 16-column block, NB = 2 blocks per wave (1
-  // when that would exceed kMaxGroup), so G = W * NB * (16 / g) sequences share an item.
+  // Prefix items (cascade schedules): the item attends one KV head; a column is (sequence,
+  // query head of that head), 16 / g sequences per 16-column block and two blocks, so
+  // G = 2 * (16 / g) sequences share an item.
   const int i_spb = 16 / g, i_sib = lr / g, i_gi = lr - i_sib * g;
-  const int i_nb = W * 2 * i_spb <= kMaxGroup ? 2 : 1;
   struct ItemRegs {
     int hv = 0;
     int pid[2] = {0, 0};
@@ -139,11 +138,54 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     r.hv = pr[lane];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int e = (i_nb * wave + k) * i_spb + i_sib;
+      const int e = k * i_spb + i_sib;
       r.sv[k] = *reinterpret_cast<const int4*>(pr + kPrecSegOff + 4 * (e < kMaxGroup ? e : kMaxGroup - 1));
       r.pid[k] = pr[kPrecPidOff + 64 * k + lane];
     }
     return r;
+  };
+  // Item pages: one head's K and V rows of 16 tokens each (TILE1 bytes per half); a wave's unit
+  // buffer holds SPW = HB such pages, and a step takes NPS of them.
+  constexpr int RB1 = D * 2, CPR1 = RB1 / 16, RPI1 = 64 / CPR1, NI1 = 16 / RPI1, TILE1 = 16 * RB1;
+  constexpr int SPW = 2 * TILE / (2 * TILE1);
+  constexpr int NPS = SPW >= 2 ? 2 : 1;
+  static_assert(SPW >= 1 && MT * 1024 <= 2 * TILE, "prefix item buffers");
+  auto item_plen = [&](const ItemRegs& r) __attribute__((always_inline)) -> int {
+    const int v = __builtin_amdgcn_readlane(r.hv, kHdrLen);
+    return v < 0 ? 0 : (v > kItemPages ? kItemPages : v);
+  };
+  auto item_head = [&](const ItemRegs& r) __attribute__((always_inline)) -> int {
+    const int v = __builtin_amdgcn_readlane(r.hv, kHdrHead);
+    return v < 0 ? 0 : (v >= P.hkv ? P.hkv - 1 : v);
+  };
+  // page p's id (p wave-uniform, < kItemPages)
+  auto item_pid = [&](const ItemRegs& r, int p) __attribute__((always_inline)) -> int {
+    return __builtin_amdgcn_readlane(p < 64 ? r.pid[0] : r.pid[1], p & 63);
+  };
+  // The K (or V) rows of step j's pages of this wave into their slots: the wave takes pages
+  // wave, wave + W, ...; step j holds its pages NPS j .. NPS j + NPS - 1, the i-th in slot i
+  // (K rows, then V rows), copied with the cached policy (every group of the run reads them).
+  auto item_issue = [&](const ItemRegs& r, int plen, int hd, int j, bool isv) __attribute__((always_inline)) {
+    const int nmine = plen > wave ? (plen - 1 - wave) / W + 1 : 0;
+    const T* base = isv ? vc : kc;
+    char* wb = smem + wave * 2 * TILE;
+#pragma unroll
+    for (int x = 0; x < NPS; ++x) {
+      const int li = NPS * j + x;
+      if (li >= nmine) break;
+      const int pid = item_pid(r, wave + W * li);
+      const int64_t pg = page_ok(pid) ? pid : 0;
+      const T* pb = base + pg * P.page_stride + (int64_t)hd * D;
+      char* dst = wb + x * 2 * TILE1 + (isv ? TILE1 : 0);
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int i = 0; i < NI1; ++i) {
+        const int t = i * RPI1 + ln / CPR1, pos = ln % CPR1;
+        const int col = pos ^ (isv ? vx<RB1>(t) : kx<RB1>(t));
+        dma16(pb + (t * rowstride32 + 8 * col), dst + i * 1024);
+      }
+    }
   };
 
   const int N0 = P.num_ctas;
@@ -171,7 +213,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   // ... and, once the head is in, this wave's first unit: HBM then streams the first pages while
   // the set-up code runs (the range loop takes them over as its first unit)
   int cpid0 = 0;
-  bool unit0 = false;
+  bool unit0 = false, item0 = false;  // the first range's first unit, or its item's first pages, issued
   if (early) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // the head is in (compiler-visible vmcnt(0))
     int len0 = __builtin_amdgcn_readlane(hv0, kHdrLen);
@@ -181,6 +223,16 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     bool plain = w0 < __builtin_amdgcn_readlane(hv0, kHdrRanges) && nseg0 > 0;
     if constexpr (CASC) plain = plain && !__builtin_amdgcn_readlane(hv0, kHdrPrefix);
     const int pi0 = active ? j : len0;
+    if constexpr (CASC) {
+      // a range that carries a prefix item: the item's first pages go out now, and stream in
+      // while the set-up code runs
+      if (w0 < __builtin_amdgcn_readlane(hv0, kHdrRanges) && __builtin_amdgcn_readlane(hv0, kHdrPrefix)) {
+        const int pl0 = item_plen(ir0), hd0 = item_head(ir0);
+        item_issue(ir0, pl0, hd0, 0, false);
+        item_issue(ir0, pl0, hd0, 0, true);
+        item0 = true;
+      }
+    }
     if (plain && pi0 < len0) {
       const int raw = __builtin_amdgcn_readlane(pv0, pi0);
       cpid0 = pid_page(raw);
@@ -231,42 +283,33 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
   };
 
   // ---- prefix item (decode_sched.h): G sequences x one chunk of pages x one KV head, all
-  // shared.  The head's K and V rows of the chunk's pages (tiles of 16 rows of D elements)
-  // stream through a ring of NS = W * HB page slots in the unit buffers: page p is copied by
-  // wave p % W into slot p % NS with the cached policy (every group of the run reads the chunk),
-  // and a wave may have NS / W pages in flight.  The pages are processed two at a time, with
-  // one barrier per step that publishes the step's pages (their copiers waited for them) and
-  // frees the slots of the previous step for the pages NS ahead.
-  // Every wave attends head h: a column is (sequence, query head of h), 16 / g sequences per
-  // 16-column block, and a wave takes NB = 2 blocks (1 when that would exceed kMaxGroup), so
-  // each K/V fragment read from LDS feeds NB products; G = W * NB * (16 / g).
-  constexpr int RB1 = D * 2, CPR1 = RB1 / 16, RPI1 = 64 / CPR1, NI1 = 16 / RPI1, TILE1 = 16 * RB1;
-  constexpr int NSP = W * 2 * TILE / (2 * TILE1);      // ring slots (pages)
-  static_assert(NSP >= 4 && NSP % W == 0 && NSP / W <= 4, "prefix ring");
+  // shared.  A column of the products is (sequence, query head of the item's head): 16 / g
+  // sequences per 16-column block and two blocks, so G = 2 * (16 / g) sequences share each K/V
+  // fragment read from LDS.  The chunk's pages are dealt to the waves like a range's (wave r
+  // takes pages r, r + W, ...); each wave streams its own pages into its own unit buffer (HB page
+  // slots of one head's K and V rows, copied with the cached policy: every group of the run reads
+  // the chunk) and attends all G sequences to them, two pages a step, with no barrier until the
+  // end, where the W states of each column are folded through LDS in wave order.
   const float scale = P.scale_log2;
   auto prefix_item = [&](int w, bool pre) __attribute__((always_inline)) {
     // the record: requested at the kernel's start for the first range, else now
     const ItemRegs ir = pre ? ir0 : load_item(w);
     if (!pre) __builtin_amdgcn_s_waitcnt(0x0F70);
-    const int hv2 = ir.hv;
-    int plen = __builtin_amdgcn_readlane(hv2, kHdrLen);
-    plen = plen < 0 ? 0 : (plen > kItemPages ? kItemPages : plen);
-    int pn = __builtin_amdgcn_readlane(hv2, kHdrNseg);
+    const int plen = item_plen(ir), hd = item_head(ir);
+    int pn = __builtin_amdgcn_readlane(ir.hv, kHdrNseg);
     pn = pn < 0 ? 0 : (pn > kMaxGroup ? kMaxGroup : pn);
-    int hd = __builtin_amdgcn_readlane(hv2, kHdrHead);
-    hd = hd < 0 ? 0 : (hd >= P.hkv ? P.hkv - 1 : hd);
     if (nsplit + kMaxGroup > kMaxSplit) flush_splits(true);  // room for this item's arrivals
     lds_barrier();  // the previous readers of the unit buffers are done
-    // my columns and their sequences (segment e = (NB wave + k) * spb + column / g)
-    const int spb = i_spb, sib = i_sib, gi = i_gi, nb = i_nb;
+    // my columns and their sequences (segment e = k * spb + column / g)
+    const int spb = i_spb, sib = i_sib, gi = i_gi;
     const int qhd = hd * g + gi;                        // query head of my column
     Seg sgk[2];
     bool ok[2];
     uint4 qk2[2][KSH];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int e = (nb * wave + k) * spb + sib;
-      ok[k] = k < nb && sib < spb && e < pn;
+      const int e = k * spb + sib;
+      ok[k] = sib < spb && e < pn;
       sgk[k] = unpack_seg(ir.sv[k], plen, B, P.slot_cap);
       const T* src = qall + (int64_t)sgk[k].b * P.q_sn + (int64_t)qhd * P.q_sh + 8 * lg;
 #pragma unroll
@@ -282,62 +325,38 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       pm[k] = -INFINITY;
       pl[k] = 0.f;
     }
-    const bool any = __ballot(ok[0] || ok[1]) != 0;
-    // page p's id (p wave-uniform, < kItemPages)
-    auto pid_at = [&](int p) __attribute__((always_inline)) -> int {
-      return __builtin_amdgcn_readlane(p < 64 ? ir.pid[0] : ir.pid[1], p & 63);
+    auto pid_at = [&](int p) __attribute__((always_inline)) -> int { return item_pid(ir, p); };
+    const int nmine = plen > wave ? (plen - 1 - wave) / W + 1 : 0;
+    const int nsteps = (nmine + NPS - 1) / NPS;
+    char* wbuf = smem + wave * 2 * TILE;
+    // (the query rows' loads were issued before the pages': the compiler's wait for them, at
+    // their first use, also covers these copies)
+    auto issue_half = [&](int j, bool isv) __attribute__((always_inline)) { item_issue(ir, plen, hd, j, isv); };
+    // vmcnt allowing the copies of n pages (of one half) to stay in flight
+    auto wait_pages = [&](int n) __attribute__((always_inline)) {
+      if (n <= 0) wait_vm<0>();
+      else if (n == 1) wait_vm<NI1>();
+      else wait_vm<2 * NI1>();
     };
-    // one head's K and V rows of page p into its ring slot (the query rows' loads were issued
-    // first: the compiler's wait for them, at their first use, also covers these copies)
-    const int64_t hoff = (int64_t)hd * D;
-    auto issue_page = [&](int p) __attribute__((always_inline)) {
-      const int pid = pid_at(p);
-      const int64_t pg = page_ok(pid) ? pid : 0;
-      char* dst = smem + (p % NSP) * 2 * TILE1;
-      const T* kb = kc + pg * P.page_stride + hoff;
-      const T* vb = vc + pg * P.page_stride + hoff;
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-#pragma unroll
-        for (int i = 0; i < NI1; ++i) {
-          const int t = i * RPI1 + ln / CPR1, pos = ln % CPR1;
-          const int col = pos ^ (x ? vx<RB1>(t) : kx<RB1>(t));
-          dma16((x ? vb : kb) + (t * rowstride32 + 8 * col), dst + x * TILE1 + i * 1024);
-        }
-      }
+    auto pages_of = [&](int j) __attribute__((always_inline)) -> int {
+      return j < nsteps ? min(NPS, nmine - NPS * j) : 0;
     };
-    constexpr int step = 2;
-    for (int p = wave; p < NSP - step && p < plen; p += W) issue_page(p);
-    for (int p0 = 0; p0 < plen; p0 += step) {
-      const int np2 = min(step, plen - p0);            // pages this step (1 or 2)
-      // the copier of each of this step's pages waits for it; its later pages (p + W, ...)
-      // already issued stay in flight (copies complete in issue order)
-      const int issued = min(plen, p0 + NSP - step);
-      const int mine_p = wave == p0 % W ? p0 : ((np2 == 2 && wave == (p0 + 1) % W) ? p0 + 1 : -1);
-      if (mine_p >= 0) {
-        const int newer = mine_p + W < issued ? (issued - 1 - mine_p) / W : 0;
-        if (newer == 0) wait_vm<0>();
-        else if (newer == 1) wait_vm<2 * NI1>();
-        else if (newer == 2) wait_vm<4 * NI1>();
-        else wait_vm<6 * NI1>();
-      }
-      lds_barrier();
-      for (int q = p0 + NSP - step; q < p0 + NSP && q < plen; ++q)
-        if (wave == q % W) issue_page(q);
-      const int pid0 = pid_at(p0);
-      const int pid1 = np2 == 2 ? pid_at(p0 + 1) : pid0;
+    if (nsteps > 0 && !(pre && item0)) {  // (the first range's went out at the start)
+      issue_half(0, false);
+      issue_half(0, true);
+    }
+    for (int j = 0; j < nsteps; ++j) {
+      const int np2 = pages_of(j);
+      const int pid0 = pid_at(wave + W * (NPS * j));
+      const int pid1 = np2 == 2 ? pid_at(wave + W * (NPS * j + 1)) : pid0;
       const bool v0 = page_ok(pid0), v1 = np2 == 2 && page_ok(pid1);
-      if (!any) continue;
-      // Straight-line step (no branch between the LDS reads and their products, so they can
-      // all be in flight together): both pages and both blocks always; the second page's slot
-      // may hold stale rows (a lone last page) and a page outside the pool holds page 0's rows,
-      // so their scores are replaced by -inf and their V fragments by zeros, by selects.
-      const char* kb0 = smem + (p0 % NSP) * 2 * TILE1;
-      const char* kb1 = smem + ((p0 + 1) % NSP) * 2 * TILE1;
-      // lane-derived LDS offsets are recomputed here, not kept from the kernel's start (kept,
-      // they are spilled, and their reloads would wait for every page copy in flight)
+      wait_pages(np2);  // K of step j has landed (its V may still be in flight)
+      // Straight-line step: both slots and both blocks always; a lone last page leaves slot 1
+      // stale and a page outside the pool holds page 0's rows, so their scores are replaced by
+      // -inf and their V fragments by zeros, by selects.
+      const char* kb0 = wbuf;
+      const char* kb1 = wbuf + (NPS == 2 ? 2 * TILE1 : 0);
+      // lane-derived LDS offsets are recomputed here, not kept from the kernel's start
       int l2 = lane;
       asm volatile("" : "+v"(l2));
       const int lr2 = l2 & 15, lg2 = l2 >> 4;
@@ -359,18 +378,8 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
           for (int s = 0; s < KSH; ++s) sa[x][k] = Mma<T>::qk(ka[x][s], qk2[k][s], sa[x][k]);
         }
       }
-      // V^T fragments of both pages (read now, used after the softmax)
-      const int tr_row = 4 * lg2 + (lr2 >> 2);
-      const char* vb0 = kb0 + TILE1 + tr_row * RB1 + (lr2 & 1) * 8;
-      const char* vb1 = kb1 + TILE1 + tr_row * RB1 + (lr2 & 1) * 8;
-      uint4 va[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int c = (2 * mt + ((lr2 & 3) >> 1)) ^ vx<RB1>(tr_row);
-        const uint2 a0 = lds_read_tr16(vb0 + (c << 4));
-        const uint2 a1 = lds_read_tr16(vb1 + (c << 4));
-        va[mt] = make_uint4(v0 ? a0.x : 0u, v0 ? a0.y : 0u, v1 ? a1.x : 0u, v1 ? a1.y : 0u);
-      }
+      wait_lgkm0();  // the K rows have been read: the slots' K halves can be refilled
+      issue_half(j + 1, false);
       // online softmax per block over the step's 16 or 32 tokens (every chunk page is full)
       uint4 pb[2];
 #pragma unroll
@@ -402,27 +411,75 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
         pb[k] = make_uint4(Mma<T>::pack(e8[0], e8[1]), Mma<T>::pack(e8[2], e8[3]),
                            Mma<T>::pack(e8[4], e8[5]), Mma<T>::pack(e8[6], e8[7]));
       }
-      // O^T += V^T P over the step's tokens: reduction slots 0-3 the first page, 4-7 the second
+      wait_pages(pages_of(j + 1));  // V of step j has landed (step j + 1's K may be in flight)
+      // V^T fragments of both slots: reduction slots 0-3 the first page, 4-7 the second
+      const int tr_row = 4 * lg2 + (lr2 >> 2);
+      const char* vb0 = kb0 + TILE1 + tr_row * RB1 + (lr2 & 1) * 8;
+      const char* vb1 = kb1 + TILE1 + tr_row * RB1 + (lr2 & 1) * 8;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        po[0][mt] = Mma<T>::qk(va[mt], pb[0], po[0][mt]);
-        po[1][mt] = Mma<T>::qk(va[mt], pb[1], po[1][mt]);
+        const int c = (2 * mt + ((lr2 & 3) >> 1)) ^ vx<RB1>(tr_row);
+        const uint2 a0 = lds_read_tr16(vb0 + (c << 4));
+        const uint2 a1 = lds_read_tr16(vb1 + (c << 4));
+        const uint4 va = make_uint4(v0 ? a0.x : 0u, v0 ? a0.y : 0u, v1 ? a1.x : 0u, v1 ? a1.y : 0u);
+        po[0][mt] = Mma<T>::qk(va, pb[0], po[0][mt]);
+        po[1][mt] = Mma<T>::qk(va, pb[1], po[1][mt]);
       }
+      wait_lgkm0();  // the V rows have been read: the slots' V halves can be refilled
+      issue_half(j + 1, true);
     }
-    // each block's columns: this head's share of one part of each of its sequences
+    // ---- the W waves' states of each column, folded in wave order: (max, sum) through the
+    // exchange buffer, then each block's tiles through the unit buffers (now idle), one block
+    // at a time; tile (k, mt) is folded, normalised and written by wave (k MT + mt) % W
+    float2* s_iml = reinterpret_cast<float2*>(&s_x[0][0][0]);  // [W][2][16]
+    float ltot[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) ltot[k] = sum_across_groups(pl[k]);
+    if (lg == 0) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) s_iml[(wave * 2 + k) * 16 + lr] = make_float2(pm[k], ltot[k]);
+    }
+    lds_barrier();
+    float Mk[2], Lk[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const float ltot = sum_across_groups(pl[k]);
-      if (ok[k]) {
-        const int64_t slot = (int64_t)sgk[k].slot0 + sgk[k].part;
-        const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-        const int64_t sidx = slot * P.hq + qhd;
+      float2 v[W];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), po[k][mt] * inv);
-        if (lg == 0) store_partial_ml(P, slot, qhd, pm[k], ltot);
+      for (int ww = 0; ww < W; ++ww) v[ww] = s_iml[(ww * 2 + k) * 16 + lr];
+      float M = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) M = fmaxf(M, v[ww].x);
+      const float mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) L += v[ww].y * __builtin_amdgcn_exp2f(v[ww].x - mu);
+      const float cs = __builtin_amdgcn_exp2f(pm[k] - mu);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) po[k][mt] *= cs;
+      Mk[k] = M;
+      Lk[k] = L;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (k > 0) lds_barrier();  // block 0's folds have read the buffers
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f4*>(wbuf + mt * 1024 + lane * 16) = po[k][mt];
+      lds_barrier();
+      const float inv = Lk[k] > 0.f ? 1.f / Lk[k] : 0.f;
+      const int64_t slot = (int64_t)sgk[k].slot0 + sgk[k].part;
+      const int64_t sidx = slot * P.hq + qhd;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if ((k * MT + mt) % W != wave) continue;
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ww = 0; ww < W; ++ww) acc += *reinterpret_cast<const f4*>(smem + ww * 2 * TILE + mt * 1024 + lane * 16);
+        if (ok[k]) st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), acc * inv);
+      }
+      if (wave == 0 && ok[k]) {
+        if (lg == 0) store_partial_ml(P, slot, qhd, Mk[k], Lk[k]);
         if (gi == 0 && lg == 0) {
-          const int e = (nb * wave + k) * spb + sib;
+          const int e = k * spb + sib;
           s_split[nsplit + e][0] = sgk[k].b;
           s_split[nsplit + e][1] = sgk[k].slot0;
           s_split[nsplit + e][2] = sgk[k].nparts;
@@ -431,7 +488,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       }
     }
     nsplit += pn;
-    lds_barrier();  // every wave is done with the ring; the arrivals are queued
+    lds_barrier();  // every wave is done with the buffers; the arrivals are queued
   };
 
   int rmax = P.r_cap;  // ranges of this plan (from the first record; never past the workspace)
@@ -538,7 +595,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
     float m = -INFINITY, lsum = 0.f;
     auto start_segment = [&]() __attribute__((always_inline)) {
       sg = seg_at(si);
-      if constexpr (!CASC) {
+      {
         // Fused append: the wave that will attend the page that receives the step's token
         // (range page k goes to rank k % J) copies the token's K and V rows of its head block
         // into its 1 KB of the exchange buffer now (lane l's 16 bytes at byte 16 l: K chunks,
@@ -676,7 +733,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       }
       // K of unit pi has landed (its V may still be in flight)
       wait_vm<NI>();
-      if constexpr (!CASC) {
+      {
         // Fused append at the page that receives the step's token: once the page's V and the
         // new rows (copied at the segment's start) have landed, the rows replace their row of
         // the staged K and V tiles and are written to that slot of the page in the cache.
@@ -848,12 +905,10 @@ bool decode_mfma_supported(int dtype, int d, int g, int hkv, int batch) {
   return hkv / decode_head_block(d, g, hkv) <= W;
 }
 
-// Sequences that share one prefix item, G = W * NB * (16 / g) (NB = 2 blocks per wave, 1 when
-// that would exceed kMaxGroup), or 0 when the shape cannot group.
+// Sequences that share one prefix item, G = 2 * (16 / g), or 0 when the shape cannot group.
 int decode_mfma_group(int d, int g, int hkv) {
   if (!((d == 64 || d == 128) && g >= 1 && g <= 16 && hkv >= 1)) return 0;
-  const int spb = 16 / g, nb = W * 2 * spb <= kMaxGroup ? 2 : 1;
-  const int G = W * nb * spb;
+  const int G = 2 * (16 / g);  // two 16-column blocks of 16 / g sequences each
   return G <= kMaxGroup ? G : 0;
 }
 

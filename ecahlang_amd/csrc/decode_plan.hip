@@ -147,7 +147,9 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams P)
       s1 = clip(P.indptr[b + 1]);
       if (hint && b > 0) {
         const int p0 = clip(P.indptr[b - 1]);
-        const int cap = min(s1 - s0, s0 - p0) - 1;  // each keeps a page of its own
+        // each keeps its own the pages that can receive the step's token: its last page, and the
+        // one before it when the last is empty (kv_last_page_len 0)
+        const int cap = min(s1 - s0 - (P.last[b] > 0 ? 1 : 2), s0 - p0 - (P.last[b - 1] > 0 ? 1 : 2));
         lc = P.shared[b];
         lc = lc < 0 ? 0 : (lc > cap ? cap : lc);
       }

@@ -38,9 +38,10 @@
 //   header   [len, nseg, head]                           (nseg <= G <= kMaxGroup sequences)
 //   segments nseg x int4, as above (beg = 0, end = len, part = the chunk's index)
 //   page ids the chunk's len page ids
-// The workgroup that owns the range streams the head's rows of each chunk page into LDS once,
-// and its waves attend all G sequences to them.  (One head per item: a workgroup's own load
-// rate is what bounds an item, so an item reads as little as possible for the most sequences.)  A grouped sequence's parts are its prefix chunks followed
+// The workgroup that owns the range reads the head's rows of each chunk page into LDS once (its
+// waves share the pages) and attends all G = 2 * (16 / g) sequences to them, so a grouped
+// sequence has one prefix part per chunk (a chunk holds up to kItemPages pages).  A grouped
+// sequence's parts are its prefix chunks followed
 // by its suffix ranges, merged like any split sequence.
 #pragma once
 #include <stdint.h>
@@ -80,14 +81,15 @@ constexpr int kPrecSegOff = 16;                        // <= kMaxGroup segments:
 constexpr int kPrecPidOff = 256;
 constexpr int kPrecStride = kPrecPidOff + kRangePages; // words, 256-byte multiple
 constexpr int kPrefixMinPages = 16;                    // shorter shared prefixes are not grouped
-constexpr int kPrefixChunkMin = 8;                     // pages per chunk, unless that makes too many
+constexpr int kPrefixChunkMin = 64;                    // pages per chunk, unless that makes too many
 constexpr int kMaxPrefixParts = 16;                    // chunks per prefix (more only past 16 x 128 pages)
 constexpr int kMaxPrefixNp = 31;                       // chunks per prefix at most (5 bits)
 constexpr int kItemPages = 128;                        // pages per chunk at most (ids in 2 registers a lane)
 // A prefix item's weight when the plan balances the ranges, in streamed pages (a suffix page
-// weighs 1): a fixed kPrefixItemFixed for its set-up and its arrivals, plus its C pages of one
-// head's rows times kPrefixCostNum / kPrefixCostDen (the item attends G sequences to each).
-constexpr int kPrefixCostNum = 7, kPrefixCostDen = 5, kPrefixItemFixed = 19;
+// weighs 1): a fixed kPrefixItemFixed for its set-up, its fold and its arrivals, plus its C
+// pages of one head's rows times kPrefixCostNum / kPrefixCostDen (the workgroup's waves share
+// the pages, each attending all G sequences to its own).
+constexpr int kPrefixCostNum = 1, kPrefixCostDen = 4, kPrefixItemFixed = 16;
 
 // Head block of the matrix-core decode: the largest power of two HB with HB * g <= 16 query heads
 // (the MFMA's 16 columns), HB * head_dim <= 256 and HB | Hkv.

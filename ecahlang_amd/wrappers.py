@@ -105,8 +105,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
         for each sequence b >= 1, how many of its leading pages are the same pages as sequence
         b - 1's (the caller guarantees the pages agree, as it does for the rest of the page
         table): a prefix that runs of sequences share is then kept in L2 for its readers after
-        the first, and with ``cascade=True`` it is read once per group of up to 32 sequences
-        instead (include/pagedkv.h, pkv_decode_plan)."""
+        the first, and with ``cascade=True`` it is read once per group of 2 * (16 / g) sequences
+        (g = num_qo_heads / num_kv_heads) instead (include/pagedkv.h, pkv_decode_plan)."""
         _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, rope_theta)
         self._indptr = _i32(indptr, "indptr")
         self._indices = _i32(indices, "indices")

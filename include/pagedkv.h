@@ -143,9 +143,12 @@ int pkv_decode_workspace_init(void* workspace, int32_t batch, void* stream);
  * the page table).  The common prefix of a run of consecutive sequences that share at least 16
  * pages is then copied with the cached load policy, so every reader after the first finds it in
  * L2 (other pages stream past the caches).  With PKV_PLAN_CASCADE in plan_flags, the common
- * prefix is instead read once per group of up to 32 sequences (one workgroup attends the whole
- * group to it, per KV head, and the parts are merged like split sequences); the results are
- * those of the plain schedule up to the order of the fp32 summation.  AutoKVCacheManager fills
+ * prefix is instead read once per group of 2 * (16 / g) sequences, g = num_qo_heads /
+ * num_kv_heads (one workgroup attends the group to each chunk of up to 64 prefix pages, per KV
+ * head, and the parts are merged like split sequences); the results are those of the plain
+ * schedule up to the order of the fp32 summation.  Each sequence keeps as its own the page
+ * that receives the step's token (its last page, and the one before an empty last page), so
+ * the fused append of pkv_batch_decode_append works with either plan.  AutoKVCacheManager fills
  * kv_shared_pages for sequences allocated on a prefix. */
 #define PKV_PLAN_CASCADE 1
 int pkv_decode_plan(const int32_t* kv_indptr, const int32_t* kv_indices, int64_t num_indices,
