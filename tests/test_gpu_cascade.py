@@ -1,7 +1,8 @@
 """Shared prefixes in the matrix-core decode (plan's kv_shared_pages): sequences in runs that
 share their leading pages, with prefixes from 16 pages (the smallest that is grouped) past 2048
-pages (more than four chunks of up to 512), runs of 1 to 17 sequences (partial groups), hints
-that understate the sharing, and head layouts whose prefix items group 8, 16 and 32 sequences.
+pages (past sixteen chunks of 64 pages, where chunks grow towards 128), runs of 1 to 17
+sequences (partial groups), hints
+that understate the sharing, and head layouts whose prefix items group 2, 4 and 8 sequences.
 With the hint alone the shared pages only change load policy, so the output is bit-identical
 to the plain schedule's; with the cascade every output row is checked against the float64
 oracle and against the plain schedule."""
@@ -71,11 +72,11 @@ QWEN_RUNS = [(1, 0, 0), (2, 16, 16), (9, 100, 100), (8, 17, 16), (17, 600, 600),
 
 
 @pytest.mark.parametrize("hq,hkv,d,dtype,runs,group", [
-    (16, 2, 128, torch.float16, QWEN_RUNS + [(40, 64, 64)], 32),             # Qwen2.5-3B
-    (32, 8, 128, torch.bfloat16, [(5, 40, 40), (1, 0, 0), (3, 20, 20)], 32), # Llama-3.1-8B
-    (32, 8, 64, torch.float16, [(6, 33, 33), (2, 70, 70)], 32),              # Llama-3.2-1B
-    (16, 1, 128, torch.bfloat16, [(10, 50, 50), (3, 16, 16)], 16),           # one KV head, g 16
-    (8, 2, 64, torch.float16, [(11, 64, 64)], 32),                           # 256-byte unit rows
+    (16, 2, 128, torch.float16, QWEN_RUNS + [(40, 64, 64)], 4),              # Qwen2.5-3B
+    (32, 8, 128, torch.bfloat16, [(5, 40, 40), (1, 0, 0), (3, 20, 20)], 8),  # Llama-3.1-8B
+    (32, 8, 64, torch.float16, [(6, 33, 33), (2, 70, 70)], 8),               # Llama-3.2-1B
+    (16, 1, 128, torch.bfloat16, [(10, 50, 50), (3, 16, 16)], 2),            # one KV head, g 16
+    (8, 2, 64, torch.float16, [(11, 64, 64)], 8),                            # 256-byte unit rows
 ])
 @torch.no_grad()
 def test_cascade_matches_oracle_and_plain_schedule(hq, hkv, d, dtype, runs, group):
