@@ -429,8 +429,8 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       issue_half(j + 1, true);
     }
     // ---- the W waves' states of each column, folded in wave order: (max, sum) through the
-    // exchange buffer, then each block's tiles through the unit buffers (now idle), one block
-    // at a time; tile (k, mt) is folded, normalised and written by wave (k MT + mt) % W
+    // exchange buffer, then the blocks' tiles through the unit buffers (now idle); tile (k, mt)
+    // is folded, normalised and written by wave (k MT + mt) % W
     float2* s_iml = reinterpret_cast<float2*>(&s_x[0][0][0]);  // [W][2][16]
     float ltot[2];
 #pragma unroll
@@ -459,31 +459,41 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeParams P) {
       Mk[k] = M;
       Lk[k] = L;
     }
+    // both blocks' tiles in one exchange when a wave's buffer holds them, else a block at a time
+    constexpr int KR = 2 * MT * 1024 <= 2 * TILE ? 2 : 1;  // blocks per exchange round
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      if (k > 0) lds_barrier();  // block 0's folds have read the buffers
+    for (int k0 = 0; k0 < 2; k0 += KR) {
+      if (k0 > 0) lds_barrier();  // the previous round's folds have read the buffers
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f4*>(wbuf + mt * 1024 + lane * 16) = po[k][mt];
+      for (int kk = 0; kk < KR; ++kk)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          *reinterpret_cast<f4*>(wbuf + (kk * MT + mt) * 1024 + lane * 16) = po[k0 + kk][mt];
       lds_barrier();
-      const float inv = Lk[k] > 0.f ? 1.f / Lk[k] : 0.f;
-      const int64_t slot = (int64_t)sgk[k].slot0 + sgk[k].part;
-      const int64_t sidx = slot * P.hq + qhd;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if ((k * MT + mt) % W != wave) continue;
-        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+      for (int kk = 0; kk < KR; ++kk) {
+        const int k = k0 + kk;
+        const float inv = Lk[k] > 0.f ? 1.f / Lk[k] : 0.f;
+        const int64_t slot = (int64_t)sgk[k].slot0 + sgk[k].part;
+        const int64_t sidx = slot * P.hq + qhd;
 #pragma unroll
-        for (int ww = 0; ww < W; ++ww) acc += *reinterpret_cast<const f4*>(smem + ww * 2 * TILE + mt * 1024 + lane * 16);
-        if (ok[k]) st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), acc * inv);
-      }
-      if (wave == 0 && ok[k]) {
-        if (lg == 0) store_partial_ml(P, slot, qhd, Mk[k], Lk[k]);
-        if (gi == 0 && lg == 0) {
-          const int e = k * spb + sib;
-          s_split[nsplit + e][0] = sgk[k].b;
-          s_split[nsplit + e][1] = sgk[k].slot0;
-          s_split[nsplit + e][2] = sgk[k].nparts;
-          s_split[nsplit + e][3] = sgk[k].nparts + sgk[k].np * (P.hkv - 1);
+        for (int mt = 0; mt < MT; ++mt) {
+          if ((k * MT + mt) % W != wave) continue;
+          f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ww = 0; ww < W; ++ww)
+            acc += *reinterpret_cast<const f4*>(smem + ww * 2 * TILE + (kk * MT + mt) * 1024 + lane * 16);
+          if (ok[k]) st_dev4(P.part_o, (uint32_t)((sidx * D + 16 * mt + 4 * lg) * sizeof(float)), acc * inv);
+        }
+        if (wave == 0 && ok[k]) {
+          if (lg == 0) store_partial_ml(P, slot, qhd, Mk[k], Lk[k]);
+          if (gi == 0 && lg == 0) {
+            const int e = k * spb + sib;
+            s_split[nsplit + e][0] = sgk[k].b;
+            s_split[nsplit + e][1] = sgk[k].slot0;
+            s_split[nsplit + e][2] = sgk[k].nparts;
+            s_split[nsplit + e][3] = sgk[k].nparts + sgk[k].np * (P.hkv - 1);
+          }
         }
       }
     }

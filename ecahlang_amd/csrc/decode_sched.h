@@ -89,7 +89,7 @@ constexpr int kItemPages = 128;                        // pages per chunk at mos
 // weighs 1): a fixed kPrefixItemFixed for its set-up, its fold and its arrivals, plus its C
 // pages of one head's rows times kPrefixCostNum / kPrefixCostDen (the workgroup's waves share
 // the pages, each attending all G sequences to its own).
-constexpr int kPrefixCostNum = 1, kPrefixCostDen = 4, kPrefixItemFixed = 16;
+constexpr int kPrefixCostNum = 1, kPrefixCostDen = 4, kPrefixItemFixed = 29;
 
 // Head block of the matrix-core decode: the largest power of two HB with HB * g <= 16 query heads
 // (the MFMA's 16 columns), HB * head_dim <= 256 and HB | Hkv.
