@@ -55,11 +55,12 @@ def _check_layer(loop, layer, rows, idx, ptr, last):
 
 
 @pytest.mark.parametrize("hint,cascade,device_steps", [(True, False, False), (False, False, False),
-                                                       (True, True, False), (True, False, True)])
+                                                       (True, True, False), (True, False, True),
+                                                       (True, True, True)])
 def test_small_loop_matches_oracle_every_step(hint, cascade, device_steps):
     """With the manager's shared-prefix hint (the prefix's pages kept in L2), without it, with
-    the cascade (the prefix read once per group), and with the whole step in the graph (the
-    page-table step on the device)."""
+    the cascade (the prefix read once per group), with the whole step in the graph (the
+    page-table step on the device), and with both (the shared-prefix step's bench setting)."""
     loop = workloads.SharedPrefixDecodeLoop(DEV, layers=3, batch=16, prefix_tokens=256, suffix=(1, 200),
                                             finish=4, max_steps=12, seed=7, record=True,
                                             shared_hint=hint, cascade=cascade, device_steps=device_steps)
