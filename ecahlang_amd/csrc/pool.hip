@@ -24,6 +24,9 @@
 //                       the bucket (manager.py:228-253), with the per-slot page counts and
 //                       last-page lengths kept on the device, so the step can be replayed from
 //                       a graph with no host work in between
+//   pkv_pool_steps_begin <- the hand-over of a batch to those steps (begin_device_steps, an
+//                       extension): the device's page counts, last-page lengths and free count
+//                       set from the bucket's metadata in one launch
 #include "common.h"
 #include "../../include/pagedkv.h"
 
@@ -39,42 +42,50 @@ namespace {
 //   kind 3, copy on write: the page table[row][col] is replaced by stack[pos - 1] (one pop),
 //           and pairs[2n], pairs[2n + 1] = (old page, new page) for the data copy
 // Operations that fall outside the stack, the table or the pairs are skipped and counted in
-// *err.
-__global__ void pool_apply_kernel(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
-                                  int32_t rows, const int32_t* ops, int32_t n_ops, int32_t* pairs,
-                                  int32_t pairs_cap, int32_t* err) {
-  __shared__ int32_t s_op[5];
-  for (int i = 0; i < n_ops; ++i) {
-    if (threadIdx.x < 5) s_op[threadIdx.x] = ops[5 * i + threadIdx.x];
+// *err.  The operations are staged in LDS a chunk at a time, so each one costs its own loads,
+// its stores and a barrier.
+constexpr int kApplyThreads = 256, kApplyChunk = 1024;
+__global__ __launch_bounds__(kApplyThreads) void pool_apply_kernel(
+    int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride, int32_t rows, const int32_t* ops,
+    int32_t n_ops, int32_t* pairs, int32_t pairs_cap, int32_t* err) {
+  __shared__ int s_op[kApplyChunk * 5];
+  const int tid = threadIdx.x;
+  for (int base = 0; base < n_ops; base += kApplyChunk) {
+    const int cnt = n_ops - base < kApplyChunk ? n_ops - base : kApplyChunk;
+    __syncthreads();  // (the previous chunk is done with s_op)
+    for (int t = tid; t < 5 * cnt; t += kApplyThreads) s_op[t] = ops[5 * (int64_t)base + t];
     __syncthreads();
-    const int kind = s_op[0], row = s_op[1], pos = s_op[2], col = s_op[3], n = s_op[4];
-    bool ok = kind >= 0 && kind <= 3 && row >= 0 && row < rows && col >= 0 && n >= 0;
-    if (kind == 0) ok = ok && (int64_t)col + n <= stride && pos - n >= 0 && pos <= stack_size;
-    else if (kind == 1) ok = ok && (int64_t)col + n <= stride && pos >= 0 && pos + n <= stack_size;
-    else if (kind == 2) ok = ok && (int64_t)col + n <= stride && pos >= 0 && pos < rows && pos != row;
-    else ok = ok && col < stride && pos >= 1 && pos <= stack_size && pairs && n < pairs_cap;
-    if (!ok) {
-      if (threadIdx.x == 0 && err) atomicAdd(err, 1);
-      // a rejected copy on write still owns its pair: mark it empty, so the data copy skips it
-      // rather than replaying an earlier call's pair onto a page that may have changed hands
-      if (threadIdx.x == 0 && kind == 3 && pairs && n >= 0 && n < pairs_cap) pairs[2 * n] = pairs[2 * n + 1] = -1;
-    } else if (kind == 3) {
-      if (threadIdx.x == 0) {
-        int32_t* cell = table + (int64_t)row * stride + col;
-        pairs[2 * n] = *cell;
-        pairs[2 * n + 1] = stack[pos - 1];
-        *cell = stack[pos - 1];
+    for (int i = 0; i < cnt; ++i) {
+      const int* o = s_op + 5 * i;
+      const int kind = o[0], row = o[1], pos = o[2], col = o[3], n = o[4];
+      bool ok = kind >= 0 && kind <= 3 && row >= 0 && row < rows && col >= 0 && n >= 0;
+      if (kind == 0) ok = ok && (int64_t)col + n <= stride && pos - n >= 0 && pos <= stack_size;
+      else if (kind == 1) ok = ok && (int64_t)col + n <= stride && pos >= 0 && pos + n <= stack_size;
+      else if (kind == 2) ok = ok && (int64_t)col + n <= stride && pos >= 0 && pos < rows && pos != row;
+      else ok = ok && col < stride && pos >= 1 && pos <= stack_size && pairs && n < pairs_cap;
+      if (!ok) {
+        if (tid == 0 && err) atomicAdd(err, 1);
+        // a rejected copy on write still owns its pair: mark it empty, so the data copy skips it
+        // rather than replaying an earlier call's pair onto a page that may have changed hands
+        if (tid == 0 && kind == 3 && pairs && n >= 0 && n < pairs_cap) pairs[2 * n] = pairs[2 * n + 1] = -1;
+      } else if (kind == 3) {
+        if (tid == 0) {
+          int32_t* cell = table + (int64_t)row * stride + col;
+          pairs[2 * n] = *cell;
+          pairs[2 * n + 1] = stack[pos - 1];
+          *cell = stack[pos - 1];
+        }
+      } else {
+        int32_t* trow = table + (int64_t)row * stride + col;
+        const int32_t* src = table + (int64_t)pos * stride;  // (kind 2 only)
+        for (int k = tid; k < n; k += kApplyThreads) {
+          if (kind == 0) trow[k] = stack[pos - 1 - k];
+          else if (kind == 1) stack[pos + k] = trow[k];
+          else trow[k] = src[k];
+        }
       }
-    } else {
-      int32_t* trow = table + (int64_t)row * stride + col;
-      const int32_t* src = table + (int64_t)pos * stride;  // (kind 2 only)
-      for (int k = threadIdx.x; k < n; k += blockDim.x) {
-        if (kind == 0) trow[k] = stack[pos - 1 - k];
-        else if (kind == 1) stack[pos + k] = trow[k];
-        else trow[k] = src[k];
-      }
+      __syncthreads();  // this operation's writes are visible to the next one
     }
-    __syncthreads();  // this operation's writes are visible to the next one
   }
 }
 
@@ -265,6 +276,30 @@ __global__ __launch_bounds__(kStepThreads) void pool_step_kernel(
   if (tid == 0) indptr[batch] = carry;
 }
 
+// The hand-over of a batch to the device steps, from the bucket's metadata as the gather wrote
+// it: rows[i] = desc[4i] for the real entries (i < real) and -1 for the padding ones; each real
+// entry's row takes npages[row] = desc[4i + 2] and plen[row] = last[i] (rows outside
+// [0, rows_total) are skipped and counted in *err); *n_free_out = n_free.
+__global__ void pool_steps_begin_kernel(const int32_t* desc, const int32_t* last, int32_t batch, int32_t real,
+                                        int32_t n_free, int32_t* rows, int32_t* npages, int32_t* plen,
+                                        int32_t rows_total, int32_t* n_free_out, int32_t* err) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) *n_free_out = n_free;
+  if (i >= batch) return;
+  if (i >= real) {
+    rows[i] = -1;
+    return;
+  }
+  const int row = desc[4 * i];
+  rows[i] = row;
+  if (row >= 0 && row < rows_total) {
+    npages[row] = desc[4 * i + 2];
+    plen[row] = last[i];
+  } else if (err) {
+    atomicAdd(err, 1);
+  }
+}
+
 }  // namespace
 
 extern "C" int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table, int64_t stride,
@@ -272,7 +307,7 @@ extern "C" int pkv_pool_apply(int32_t* stack, int32_t stack_size, int32_t* table
                               int32_t pairs_cap, int32_t* err, void* stream) {
   if (n_ops < 0 || stack_size < 0 || stride <= 0 || rows <= 0 || pairs_cap < 0) return kBadArg;
   if (n_ops == 0) return kOk;
-  hipLaunchKernelGGL(pool_apply_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, stack, stack_size,
+  hipLaunchKernelGGL(pool_apply_kernel, dim3(1), dim3(kApplyThreads), 0, (hipStream_t)stream, stack, stack_size,
                      table, stride, rows, ops, n_ops, pairs, pairs_cap, err);
   return (int)hipGetLastError();
 }
@@ -342,5 +377,17 @@ extern "C" int pkv_pool_step(int32_t* stack, int32_t* n_free, int32_t* table, in
   hipLaunchKernelGGL(pool_gather_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, table, stride,
                      rows_total, desc, kv_indptr, batch, kv_indices, num_indices, positions, page_size,
                      slots, err);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkv_pool_steps_begin(const int32_t* desc, const int32_t* last_len, int32_t batch, int32_t real,
+                                    int32_t n_free, int32_t* rows, int32_t* npages, int32_t* plen,
+                                    int32_t rows_total, int32_t* n_free_out, int32_t* err, void* stream) {
+  if (batch < 0 || real < 0 || real > batch || n_free < 0 || rows_total <= 0 || !n_free_out ||
+      (batch > 0 && (!desc || !last_len || !rows || !npages || !plen)))
+    return kBadArg;
+  const unsigned blocks = (unsigned)(batch > 0 ? (batch + 255) / 256 : 1);
+  hipLaunchKernelGGL(pool_steps_begin_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, desc, last_len,
+                     batch, real, n_free, rows, npages, plen, rows_total, n_free_out, err);
   return (int)hipGetLastError();
 }

@@ -230,6 +230,7 @@ class AutoKVCacheManager:
         if prefix_cache_rows < 0 or (prefix_cache_rows and strict_reference_q1):
             raise ValueError("prefix_cache_rows must be >= 0, and the prefix cache needs full last pages "
                              "(strict_reference_q1=False)")
+        self._mask_resets: list = []  # slots whose mask_penalty row allocate set back to 1
         self.mask_penalty = torch.ones(self.seq_lens, vocab_size, dtype=dtype, device=self.device)
 
         if total_gpu_mem_bytes is None:
@@ -316,18 +317,49 @@ class AutoKVCacheManager:
         table[:, : self._stride].copy_(self._table)
         self._table, self._stride = table, new
 
+    @property
+    def mask_penalty(self) -> torch.Tensor:
+        """manager.py:56: one row per sequence slot, set back to 1 by ``allocate``.  The resets
+        of a batch of allocations are applied together (one launch), at the next pool flush
+        or read of this attribute, on the current stream."""
+        if self._mask_resets:
+            self._reset_mask_rows(self._staging.copy(self._reset_words()), 0)
+        return self._mask_penalty
+
+    @mask_penalty.setter
+    def mask_penalty(self, value: torch.Tensor) -> None:
+        if self._mask_resets:
+            self._reset_mask_rows(self._staging.copy(self._reset_words()), 0)
+        self._mask_penalty = value
+
+    def _reset_words(self) -> list:
+        """The pending reset slots as int32 word pairs (little-endian int64 indices)."""
+        return [w for r in self._mask_resets for w in (r, 0)]
+
+    def _reset_mask_rows(self, staged: torch.Tensor, off: int) -> None:
+        idx = staged[off: off + 2 * len(self._mask_resets)].view(torch.int64)
+        self._mask_resets = []
+        self._mask_penalty.index_fill_(0, idx, 1.0)
+
     def _flush(self) -> None:
-        """Apply the queued pops, pushes and copies (one launch, in order, on the current
-        stream), then copy the K/V data of the queued copies on write."""
+        """Apply the queued pops, pushes and copies (one launch, with the effect of applying
+        them in order, on the current stream) and the queued mask_penalty resets, from one
+        staged copy; then copy the K/V data of the queued copies on write."""
         self._end_dev()
-        if not self._ops:
+        if not self._ops and not self._mask_resets:
             return
         flat = [x for op in self._ops for x in op]
+        off = len(flat) + len(flat) % 2  # (the resets' int64 words start 8-byte aligned)
+        if self._mask_resets:
+            flat += [0] * (off - len(flat)) + self._reset_words()
         ops = self._staging.copy(flat)
-        check(lib().pkv_pool_apply(self._stack.data_ptr(), self.max_blocks, self._table.data_ptr(),
-                                   self._stride, self._rows, ops.data_ptr(), len(self._ops),
-                                   self._pairs.data_ptr(), self._cow_cap, self._err.data_ptr(),
-                                   stream_ptr(self.device)), "page pool update")
+        if self._ops:
+            check(lib().pkv_pool_apply(self._stack.data_ptr(), self.max_blocks, self._table.data_ptr(),
+                                       self._stride, self._rows, ops.data_ptr(), len(self._ops),
+                                       self._pairs.data_ptr(), self._cow_cap, self._err.data_ptr(),
+                                       stream_ptr(self.device)), "page pool update")
+        if self._mask_resets:
+            self._reset_mask_rows(ops, off)
         self._ops = []
         if self._n_cow:
             c = self.kv_cache
@@ -546,7 +578,7 @@ class AutoKVCacheManager:
             page_len = bs
         self.batch_to_page_lengths[batch_id] = page_len
         self.batch_to_total_tokens[batch_id] = total_tokens
-        self.mask_penalty[slot] = 1.0
+        self._mask_resets.append(slot)  # (mask_penalty[slot] = 1: applied with the next flush or read)
         return _Pages(self, slot, k + num_pages)
 
     def free(self, batch_id, *, tokens=None) -> None:
@@ -872,16 +904,15 @@ class AutoKVCacheManager:
         if sum(self._npages[i] for i in ids) + len(ids) * grow + bucket_size - len(ids) > cap:
             raise RuntimeError("page table of the device steps larger than the bucket's kv_indices buffer")
         self.fill_cuda_graph_metadata(bucket_size, ids)
-        rows = [self.batch_to_seq_len[i] for i in ids]
         npages = [self._npages[i] for i in ids]
         plen = [self.batch_to_page_lengths[i] for i in ids]
-        staged = self._staging.copy(rows + [-1] * (bucket_size - len(ids)) + npages + plen)
-        self._cg_rows[bucket_size].copy_(staged[:bucket_size])
-        if ids:
-            idx = staged[:len(ids)].long()
-            self._dev_npages.index_copy_(0, idx, staged[bucket_size: bucket_size + len(ids)])
-            self._dev_plen.index_copy_(0, idx, staged[bucket_size + len(ids):])
-        self._dev_nfree.fill_(self._n_free)
+        # the device's counts, from the metadata just written (one launch)
+        check(lib().pkv_pool_steps_begin(self._cg_meta[bucket_size].data_ptr(),
+                                         self._cg_kv_last_page_len[bucket_size].data_ptr(), bucket_size, len(ids),
+                                         self._n_free, self._cg_rows[bucket_size].data_ptr(),
+                                         self._dev_npages.data_ptr(), self._dev_plen.data_ptr(), self._rows,
+                                         self._dev_nfree.data_ptr(), self._err.data_ptr(), stream_ptr(self.device)),
+              "device steps hand-over")
         # one token a step: a row with last-page length p pops at the steps k with p + k a
         # multiple of bs, and a row whose last page starts full (p == bs) also pops at step 1
         hist = np.zeros(bs, dtype=np.int64)

@@ -356,6 +356,16 @@ int pkv_pool_step(int32_t* stack, int32_t* n_free, int32_t* table, int64_t strid
                   int32_t* kv_indices, int64_t num_indices, int64_t max_total, int32_t* slots,
                   int32_t* err, void* stream);
 
+/* The hand-over of a batch to pkv_pool_step (AutoKVCacheManager.begin_device_steps, an
+ * extension with no counterpart in the reference), from the gather descriptor and
+ * kv_last_page_len that fill_cuda_graph_metadata wrote for the bucket: rows[i] = desc[4i] for
+ * the real entries i < real and -1 for the padding entries i < batch; npages[desc[4i]] =
+ * desc[4i + 2] and last_len[desc[4i]] = kv_last_page_len[i] for the real entries (rows outside
+ * [0, rows_total) are skipped and counted in *err, which may be NULL); *n_free_out = n_free. */
+int pkv_pool_steps_begin(const int32_t* desc, const int32_t* kv_last_page_len, int32_t batch, int32_t real,
+                         int32_t n_free, int32_t* rows, int32_t* npages, int32_t* last_len,
+                         int32_t rows_total, int32_t* n_free_out, int32_t* err, void* stream);
+
 /* Top-k / top-p sampling from logits (flashinfer.sampling.top_k_top_p_sampling_from_logits at
  * ecahlang/main.py:377-379, 400-402, 489-491, 582-584: top-k first, then top-p on the
  * renormalised top-k distribution, deterministic=True).  logits: rows x vocab (row stride in

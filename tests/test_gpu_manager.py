@@ -420,3 +420,61 @@ def test_metadata_staging_refuses_graph_capture():
     assert m.batch_to_blocks[2] == ref.batch_to_blocks[2]
     assert list(m.free_blocks) == ref.free_blocks
     assert m.pool_errors() == 0
+
+
+def test_long_operation_queue_matches_oracle():
+    """Over a thousand queued pops and pushes applied by one flush (the device stages them a
+    chunk of 1024 at a time): the same pages as the oracle's in-order lists."""
+    rng = random.Random(7)
+    P = 60
+    dev, ref = _pool(P), RefKVCacheManager(P)
+    queued = 0
+    while queued < 1300:
+        sid = rng.randrange(8)
+        if sid in ref.batch_to_blocks:
+            dev.free(sid)
+            ref.free(sid)
+            queued += 1
+        else:
+            n = rng.choice([1, 15, 16, 17, 33, 48])
+            try:
+                ref.allocate(sid, n)
+            except RuntimeError:
+                with pytest.raises(RuntimeError):
+                    dev.allocate(sid, n)
+                continue
+            dev.allocate(sid, n)
+            queued += 1
+    assert len(dev._ops) > 1024
+    _same_state(dev, ref)
+    assert dev.pool_errors() == 0
+
+
+def test_mask_penalty_rows_reset_on_allocate():
+    """manager.py:56, 110: allocate sets the sequence slot's mask_penalty row back to 1.  The
+    resets of several allocations are applied together: at the next flush of the pool (seen
+    through a tensor taken before the allocations) or at the next read of the attribute."""
+    m = AutoKVCacheManager(1, 1, 64, vocab_size=96, total_gpu_mem_bytes=64 * 16 * 64 * 2 * 2,
+                           mem_utilization=1.0, dtype=torch.float16, device=DEV, max_pages_per_seq=8)
+    t = m.mask_penalty
+    t.fill_(0.5)
+    m.allocate("a", 20)
+    m.allocate("b", 0)
+    m.get_append_metadata(["a", "b"])  # a flush
+    slots = [m.batch_to_seq_len["a"], m.batch_to_seq_len["b"]]
+    want = torch.full_like(t, 0.5)
+    want[slots] = 1.0
+    assert torch.equal(t, want)
+    t[slots] = 0.25
+    m.free("a")
+    m.allocate("c", 5)
+    m.allocate("d", 40)
+    got = m.mask_penalty  # a read, no flush
+    assert got is t
+    for s in (m.batch_to_seq_len["c"], m.batch_to_seq_len["d"]):
+        want[s] = 1.0
+    want[m.batch_to_seq_len["b"]] = 0.25
+    if m.batch_to_seq_len["c"] != slots[0] and m.batch_to_seq_len["d"] != slots[0]:
+        want[slots[0]] = 0.25
+    assert torch.equal(got, want)
+    assert m.pool_errors() == 0
