@@ -77,15 +77,6 @@ struct Targets {
     if (carry) return w * (ws + xt) / R - (cnt(w) * xt + Rp - 1) / Rp;
     return (w - cnt(w)) * ws / (R - Rp);
   }
-  // smallest w in [0, R] with tgt(w) >= x
-  __device__ int first_at_least(int64_t x) const {
-    int lo = 0, hi = R;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (tgt(mid) >= x) hi = mid; else lo = mid + 1;
-    }
-    return lo;
-  }
 };
 
 // Block-wide exclusive scan of v (all 1024 threads call it); `carry` holds the sum of the
@@ -117,6 +108,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams P)
   __shared__ int s_wsum[kPlanThreads / 64];
   __shared__ unsigned long long s_xt;
   __shared__ int s_starts[kStartsLds + 1];
+  __shared__ int64_t s_tgt[kStartsLds + 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int B = P.batch;
   if (tid == 0) {
@@ -284,14 +276,27 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams P)
   for (int pass = 0; pass < 2 && R > 0; ++pass) {
     const int c = pass == 0 ? P.seg_cost : 0;
     const Targets T((int64_t)ns + (int64_t)c * (nne > 0 ? nne - 1 : 0), pass == 0 ? XT : 0, R, Rp);
+    // every range's start weight, computed once (a thread each: three 64-bit divisions) for the
+    // searches below, when it fits in LDS
+    const bool tab = R <= kStartsLds;
+    if (tab) {
+      for (int w = tid; w <= R; w += kPlanThreads) s_tgt[w] = T.tgt(w);
+      __syncthreads();
+    }
+    auto tgt_at = [&](int w) -> int64_t { return tab ? s_tgt[w] : T.tgt(w); };
     for (int b = tid; b < B; b += kPlanThreads) {
       const int len = P.sl[b];
       if (len <= 0) continue;
       const int k = P.rank[b], pos = P.sp[b];
       const int64_t w0 = (int64_t)pos + (int64_t)c * k;
       const int64_t lo = k == 0 ? 0 : w0 - c, hi = w0 + len;
-      for (int w = T.first_at_least(lo); w < R; ++w) {
-        const int64_t tw = T.tgt(w);
+      int wl = 0, wh = R;  // smallest w in [0, R] with tgt(w) >= lo
+      while (wl < wh) {
+        const int mid = (wl + wh) >> 1;
+        if (tgt_at(mid) >= lo) wh = mid; else wl = mid + 1;
+      }
+      for (int w = wl; w < R; ++w) {
+        const int64_t tw = tgt_at(w);
         if (tw >= hi) break;
         starts[w] = tw < w0 ? pos : (int)(pos + (tw - w0));
         P.bf[w] = b;
