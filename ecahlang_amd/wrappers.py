@@ -55,6 +55,7 @@ def _unsupported(pos_encoding_mode, window_left, logits_soft_cap, rope_scale, ro
 
 _DECODE_VALU, _DECODE_DYNAMIC, _DECODE_PLANNED = 1, 2, 4  # pkv_batch_decode flags (include/pagedkv.h)
 _PLAN_CASCADE = 1  # pkv_decode_plan flag
+_INIT_COUNTERS = 8192  # decode split counters zeroed when a workspace is given
 
 class BatchDecodeWithPagedKVCacheWrapper:
     """Paged decode attention: one query token per sequence (FlashInfer contract)."""
@@ -71,7 +72,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._kv_layout = "NHD"
         self._use_cuda_graph = use_cuda_graph
         self._planned = False
-        self._counters_ready = 0  # batch size whose counters are known to be zero
+        self._zero_counters()
         # Whether this wrapper's schedules carry cascade prefix items.  run() picks the kernel
         # variant from it when it is enqueued, so a run captured in a graph keeps the variant of
         # its plan: once a run has been captured, a plan that changes it is refused (replays
@@ -85,8 +86,22 @@ class BatchDecodeWithPagedKVCacheWrapper:
 
     def reset_workspace_buffer(self, float_workspace_buffer: torch.Tensor, *_args) -> None:
         self._workspace = float_workspace_buffer
-        self._counters_ready = 0
+        self._zero_counters()
         self._captured_mode = None
+
+    def _zero_counters(self) -> None:
+        """The workspace starts with one split counter per sequence (int32), which the decode
+        leaves at zero (each sequence's last arrival resets its own).  The first
+        ``_INIT_COUNTERS`` are zeroed here, when the workspace is given, so that a plan
+        captured in a graph does not record the fill.  ``_counters_ready``: how many leading
+        counters are known to be zero; a plan's schedule overwrites the words after its own
+        batch's counters, so it lowers the count to that batch."""
+        self._counters_ready = 0
+        n = min(_INIT_COUNTERS, self._workspace.numel() * self._workspace.element_size() // 4)
+        if n > 0 and not torch.cuda.is_current_stream_capturing():
+            check(lib().pkv_decode_workspace_init(self._workspace.data_ptr(), n,
+                                                  stream_ptr(self._workspace.device)), "decode workspace")
+            self._counters_ready = n
 
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
              num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
@@ -145,7 +160,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         if self._batch > self._counters_ready:
             check(lib().pkv_decode_workspace_init(self._workspace.data_ptr(), self._batch,
                                                   stream_ptr(dev)), "decode plan")
-            self._counters_ready = self._batch
+        self._counters_ready = self._batch  # (the schedule is written after these)
         self._flags = 0 if deterministic else _DECODE_DYNAMIC
         shared = 0
         if kv_shared_pages is not None:
