@@ -99,8 +99,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._counters_ready = 0
         n = min(_INIT_COUNTERS, self._workspace.numel() * self._workspace.element_size() // 4)
         if n > 0 and not torch.cuda.is_current_stream_capturing():
-            check(lib().pkv_decode_workspace_init(self._workspace.data_ptr(), n,
-                                                  stream_ptr(self._workspace.device)), "decode workspace")
+            dev = self._workspace.device
+            check(lib().pkv_decode_workspace_init(self._workspace.data_ptr(), n, stream_ptr(dev)),
+                  "decode workspace")
+            # (complete before any stream's plan or run reads the counters)
+            torch.cuda.current_stream(dev).synchronize()
             self._counters_ready = n
 
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
