@@ -207,6 +207,31 @@ def graph_time(torch, stream, graph, reps, launches, samples=5):
     return statistics.median(times)
 
 
+def read_probe(torch, dev, stream, nbytes, nbuf, blocks, per_buf=8):
+    """Seconds per launch of the library's streaming-read probe (pkv_probe_stream_read) over
+    nbytes with `blocks` workgroups, `nbuf` buffers read in turn (more than the 256 MB MALL
+    holds, as the decode's rotated pools are), timed like the kernels: a captured graph of
+    per_buf x nbuf launches replayed back to back."""
+    from ecahlang_amd._lib import check, lib, stream_ptr
+    nb = -(-nbytes // 16) * 16
+    bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        def launch(b):
+            check(lib().pkv_probe_stream_read(b.data_ptr(), nb, blocks, sink.data_ptr(), stream_ptr(dev)),
+                  "read probe")
+        for b in bufs:
+            launch(b)
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(per_buf):
+                for b in bufs:
+                    launch(b)
+    t = graph_time(torch, stream, graph, 3, per_buf * nbuf)
+    del graph, bufs
+    return t
+
+
 def long_context(args, torch, workloads, Wrapper, dev):
     """Decode-only timing of the long-context workload (K/V far beyond the 256 MB MALL, so
     no pool rotation is needed); the CPU baseline runs on a bounded sample of sequences."""
@@ -1163,6 +1188,16 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
 
     dbytes = decode_bytes(wb)
     gbs = dbytes / t_dec / 1e9
+    # the read rate a launch of the decode's size reaches here: the same bytes (four buffers in
+    # turn), one workgroup per CU as the decode runs and the best of wider launches; and a 2 GiB
+    # read for the sustained rate
+    probe = {}
+    for blocks in (w._ctas, 2 * w._ctas, 4 * w._ctas):
+        probe[blocks] = dbytes / read_probe(torch, dev, stream, dbytes, NL, blocks) / 1e9
+    best = max(probe, key=probe.get)
+    large = 1 << 31
+    large_gbs = large / read_probe(torch, dev, stream, large, 1, 4 * w._ctas, per_buf=8) / 1e9
+    torch.cuda.synchronize()
     nnz = wb.k_new.shape[0]
     result = {
         "metric": "paged decode attn GB/s (% HBM peak) + KV append Mtok/s, Qwen2.5-3B B=64",
@@ -1197,6 +1232,19 @@ def headline(args, torch, workloads, ops, BatchDecodeWithPagedKVCacheWrapper, de
         "append_us": round(t_app * 1e6, 3),
         "append_nnz": nnz,
         "decode_append_fused_us": round(t_fused * 1e6, 3),
+        "hbm_read_probe": {
+            "kernel": "pkv_probe_stream_read (1024-thread workgroups, 8 x 16-byte non-temporal loads in "
+                      "flight per thread, contiguous slices)",
+            "bytes": dbytes,
+            "buffers_rotated": NL,
+            "gbs_at_decode_ctas": round(probe[w._ctas], 2),
+            "decode_ctas": w._ctas,
+            "best_gbs": round(probe[best], 2),
+            "best_blocks": best,
+            "large_bytes": large,
+            "large_gbs": round(large_gbs, 2),
+            "decode_frac_of_best": round(gbs / probe[best], 4),
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),

@@ -72,6 +72,7 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_pool_step": (
         _i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
                _i64, _vp, _vp, _vp]),
+    "pkv_probe_stream_read": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "pkv_pool_steps_begin": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp]),
     "pkv_top_k_top_p_sampling": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp]),
     "pkv_sampling_workspace_bytes": (_i64, [_i32, _i32]),

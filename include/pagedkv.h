@@ -405,6 +405,12 @@ int pkv_scale_logits(const void* logits, int64_t row_stride, int32_t rows, int32
                      const int32_t* penalty_rows, const float* temperature, float* out, int64_t out_stride,
                      void* stream);
 
+/* A measurement helper with no counterpart in the reference: reads `bytes` of device memory at
+ * src (16-byte aligned, a multiple of 16 bytes) with `blocks` workgroups of 1024 threads, each
+ * workgroup a contiguous slice, with 16-byte non-temporal loads; *sink (device, 4 bytes) may be
+ * written.  Timed by the caller, it gives the HBM read rate a launch of that size reaches. */
+int pkv_probe_stream_read(const void* src, int64_t bytes, int32_t blocks, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -484,3 +484,26 @@ def test_prefill_chunked_qwen_full_size(causal):
                          wb.indices.numpy(), wb.last.numpy(), wb.ps, causal=causal)
     np.testing.assert_allclose(o.float().cpu().numpy(), ref, **TOL[wb.dtype])
     np.testing.assert_allclose(ov.float().cpu().numpy(), ref, **TOL[wb.dtype])
+
+
+def test_read_probe_reads_in_bounds_and_checks_arguments():
+    """pkv_probe_stream_read (the bench's achievable-bandwidth probe): slices of any size over
+    any workgroup count, including more workgroups than 16-byte words, run and leave the guard
+    words around the buffer alone; bad arguments are refused before anything is enqueued."""
+    from ecahlang_amd._lib import lib, stream_ptr
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for words, blocks in ((1, 1), (7, 3), (1000, 256), (4099, 2048), (65536, 256)):
+        buf = torch.full((words * 4 + 8,), 0x5A5A5A5A, dtype=torch.int32, device=dev)
+        inner = buf[4: 4 + words * 4]
+        assert lib().pkv_probe_stream_read(inner.data_ptr(), words * 16, blocks, sink.data_ptr(),
+                                           stream_ptr(dev)) == 0
+        torch.cuda.synchronize()
+        assert int(sink.item()) in (0, 1)
+        assert bool((buf == 0x5A5A5A5A).all())
+    x = torch.zeros(64, dtype=torch.int32, device=dev)
+    s = stream_ptr(dev)
+    assert lib().pkv_probe_stream_read(x.data_ptr(), 24, 4, sink.data_ptr(), s) < 0      # not 16-byte words
+    assert lib().pkv_probe_stream_read(x.data_ptr() + 4, 32, 4, sink.data_ptr(), s) < 0  # misaligned
+    assert lib().pkv_probe_stream_read(x.data_ptr(), 64, 0, sink.data_ptr(), s) < 0      # no workgroups
+    assert lib().pkv_probe_stream_read(x.data_ptr(), 64, 4, 0, s) < 0                    # no sink
