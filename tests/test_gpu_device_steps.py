@@ -129,3 +129,35 @@ def test_device_steps_raise_like_the_reference_when_the_pool_runs_dry():
     assert {i: m.batch_to_page_lengths[i] for i in ids} == {i: ref.batch_to_page_lengths[i] for i in ids}
     assert list(m.free_blocks) == ref.free_blocks
     assert m.pool_errors() == 0
+
+
+def test_steps_begin_hand_over_through_the_c_abi():
+    """pkv_pool_steps_begin: from a bucket's gather descriptor and kv_last_page_len, the real
+    entries' rows go to the row list and their page counts and last-page lengths to the
+    per-row arrays, the padding entries get row -1, the free count is written, rows outside
+    the table are counted in err; a real count above the batch is refused."""
+    from ecahlang_amd._lib import lib, stream_ptr
+    dev = torch.device("cuda:0")
+    batch, real, rows_total = 6, 4, 10
+    # desc: 4 words per entry (row, column, pages, unused); entry 2 names a row outside the table
+    desc = torch.tensor([[3, 0, 5, 0], [7, 0, 1, 0], [12, 0, 2, 0], [0, 0, 9, 0], [10, 0, 1, 0], [10, 1, 1, 0]],
+                        dtype=torch.int32, device=dev).reshape(-1)
+    last = torch.tensor([16, 1, 7, 3, 1, 1], dtype=torch.int32, device=dev)
+    out_rows = torch.full((batch,), 99, dtype=torch.int32, device=dev)
+    npages = torch.full((rows_total,), -5, dtype=torch.int32, device=dev)
+    plen = torch.full((rows_total,), -5, dtype=torch.int32, device=dev)
+    nfree = torch.zeros(1, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    args = (desc.data_ptr(), last.data_ptr(), batch, real, 1234, out_rows.data_ptr(), npages.data_ptr(),
+            plen.data_ptr(), rows_total, nfree.data_ptr(), err.data_ptr(), stream_ptr(dev))
+    assert lib().pkv_pool_steps_begin(*args) == 0
+    torch.cuda.synchronize()
+    assert out_rows.tolist() == [3, 7, 12, 0, -1, -1]
+    want_np, want_pl = [-5] * rows_total, [-5] * rows_total
+    for r, n, p in ((3, 5, 16), (7, 1, 1), (0, 9, 3)):
+        want_np[r], want_pl[r] = n, p
+    assert npages.tolist() == want_np and plen.tolist() == want_pl
+    assert nfree.item() == 1234 and err.item() == 1
+    bad = list(args)
+    bad[3] = batch + 1
+    assert lib().pkv_pool_steps_begin(*bad) < 0
